@@ -1,0 +1,195 @@
+// The HIP flavour of include/layover_transfer.h for MI355X (gfx950). Replaces the reference's
+// native/transfer_cuda.cu: the same engine (transfer_engine.h) over HIP streams, events,
+// SDMA copies (hipMemcpyAsync to and from pinned memory) and this file's gather and scatter
+// kernels.
+//
+// One HIP runtime per process. torch ships its own libamdhip64.so.7 and loads it first; this
+// library's NEEDED entry has the same soname, so the dynamic linker binds it to torch's copy
+// and pool pointers, streams and events are the same objects on both sides. check_pool
+// proves it on every transfer (reference transfer_cuda.cu:58-65 does the same for CUDA).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <stdexcept>
+#include <string>
+
+#include "layover_transfer.h"
+
+namespace lt {
+
+// Block copy kernels. One workgroup of 256 lanes moves one 64 KiB chunk of one block:
+// grid.x = chunks_per_block * blocks, flattened, so there is no grid-y limit to respect.
+// Lane l moves words l, l + 256, ... of its chunk: each wave instruction touches 64
+// consecutive words (1 KiB with 16-byte words), which the memory system serves as whole
+// cache lines. 16-byte words when pool, staging and block_bytes allow it, else 8-byte words
+// (the ABI only promises 8-byte alignment).
+constexpr uint32_t kCopyLanes = 256;
+typedef uint32_t Word16 __attribute__((ext_vector_type(4)));
+typedef uint32_t Word8 __attribute__((ext_vector_type(2)));
+constexpr uint64_t kCopyChunk = 64 * 1024;
+
+template <class Word>
+__device__ __forceinline__ void copy_chunk(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, uint64_t bytes) {
+    const Word* from = reinterpret_cast<const Word*>(src);
+    Word* to = reinterpret_cast<Word*>(dst);
+    const uint32_t words = uint32_t(bytes / sizeof(Word));
+#pragma unroll 4
+    for (uint32_t w = threadIdx.x; w < words; w += kCopyLanes) to[w] = __builtin_nontemporal_load(from + w);
+}
+
+template <class Word>
+__global__ __launch_bounds__(kCopyLanes) void gather_blocks(const uint8_t* __restrict__ pool, const uint32_t* __restrict__ ids,
+                                                             uint8_t* __restrict__ staging, uint64_t block_bytes,
+                                                             uint32_t chunks_per_block) {
+    const uint32_t index = blockIdx.x / chunks_per_block;
+    const uint64_t offset = uint64_t(blockIdx.x % chunks_per_block) * kCopyChunk;
+    const uint64_t bytes = block_bytes - offset < kCopyChunk ? block_bytes - offset : kCopyChunk;
+    copy_chunk<Word>(pool + uint64_t(ids[index]) * block_bytes + offset, staging + uint64_t(index) * block_bytes + offset, bytes);
+}
+
+template <class Word>
+__global__ __launch_bounds__(kCopyLanes) void scatter_blocks(uint8_t* __restrict__ pool, const uint32_t* __restrict__ ids,
+                                                              const uint8_t* __restrict__ staging, uint64_t block_bytes,
+                                                              uint32_t chunks_per_block) {
+    const uint32_t index = blockIdx.x / chunks_per_block;
+    const uint64_t offset = uint64_t(blockIdx.x % chunks_per_block) * kCopyChunk;
+    const uint64_t bytes = block_bytes - offset < kCopyChunk ? block_bytes - offset : kCopyChunk;
+    copy_chunk<Word>(staging + uint64_t(index) * block_bytes + offset, pool + uint64_t(ids[index]) * block_bytes + offset, bytes);
+}
+
+class HipDevice {
+   public:
+    using Stream = hipStream_t;
+    using Event = hipEvent_t;
+
+    static const char* flavor() { return "hip"; }
+    static Stream stream_from_handle(void* handle) { return static_cast<Stream>(handle); }
+
+    explicit HipDevice(int device) : device_(device) {
+        int count = 0;
+        check(hipGetDeviceCount(&count), "hipGetDeviceCount");
+        if (device < 0 || device >= count)
+            throw std::invalid_argument("device " + std::to_string(device) + " does not exist (" + std::to_string(count) + " visible)");
+        activate();
+    }
+
+    // The scheduler may call from any thread; the current device is per thread.
+    void activate() { check(hipSetDevice(device_), "hipSetDevice"); }
+
+    void prepare_teardown() {}
+
+    // A kernel given host memory or another device's memory as the pool would fault the GPU.
+    void check_pool(const void* pool) {
+        hipPointerAttribute_t attributes{};
+        const hipError_t status = hipPointerGetAttributes(&attributes, pool);
+        if (status != hipSuccess) (void)hipGetLastError();  // unknown to HIP: plain host memory
+        if (status != hipSuccess || attributes.type != hipMemoryTypeDevice || attributes.device != device_) {
+            throw std::invalid_argument("pool is not memory of HIP device " + std::to_string(device_) +
+                                        ": it is host memory, another device's, or unknown to this HIP runtime");
+        }
+    }
+
+    void* device_alloc(uint64_t bytes) {
+        void* pointer = nullptr;
+        check(hipMalloc(&pointer, bytes), "hipMalloc");
+        return pointer;
+    }
+    void device_free(void* pointer) { check(hipFree(pointer), "hipFree"); }
+
+    // Null when the host is out of memory, which the engine survives.
+    void* host_alloc(uint64_t bytes) {
+        void* pointer = nullptr;
+        const hipError_t status = hipHostMalloc(&pointer, bytes, hipHostMallocDefault);
+        if (status == hipErrorOutOfMemory || status == hipErrorMemoryAllocation) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        check(status, "hipHostMalloc");
+        return pointer;
+    }
+    void host_free(void* pointer) { check(hipHostFree(pointer), "hipHostFree"); }
+
+    // Non-blocking, default priority: torch's null stream must not serialize against the copy
+    // stream, or decode would wait for every transfer in flight.
+    Stream stream_create() {
+        Stream stream = nullptr;
+        check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+        return stream;
+    }
+    void stream_sync(Stream stream) { check(hipStreamSynchronize(stream), "hipStreamSynchronize"); }
+    void stream_destroy(Stream stream) { check(hipStreamDestroy(stream), "hipStreamDestroy"); }
+
+    Event event_create() {
+        Event event = nullptr;
+        check(hipEventCreateWithFlags(&event, hipEventDisableTiming), "hipEventCreateWithFlags");
+        return event;
+    }
+    void event_destroy(Event event) { check(hipEventDestroy(event), "hipEventDestroy"); }
+    void event_record(Event event, Stream stream) { check(hipEventRecord(event, stream), "hipEventRecord"); }
+    void stream_wait(Stream stream, Event event) { check(hipStreamWaitEvent(stream, event, 0), "hipStreamWaitEvent"); }
+
+    bool event_query(Event event) {
+        const hipError_t status = hipEventQuery(event);
+        if (status == hipErrorNotReady) return false;
+        check(status, "hipEventQuery");
+        return true;
+    }
+    void event_sync(Event event) { check(hipEventSynchronize(event), "hipEventSynchronize"); }
+
+    void memcpy_to_host(Stream stream, void* dst, const void* src, uint64_t bytes) {
+        check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, stream), "hipMemcpyAsync(device to host)");
+    }
+    void memcpy_to_device(Stream stream, void* dst, const void* src, uint64_t bytes) {
+        check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream), "hipMemcpyAsync(host to device)");
+    }
+
+    void launch_gather(Stream stream, const uint8_t* pool, const uint32_t* ids, uint8_t* staging, uint64_t block_bytes, uint32_t blocks) {
+        const uint32_t chunks = chunks_for(block_bytes);
+        const dim3 grid(chunks * blocks);
+        if (wide(pool, staging, block_bytes))
+            hipLaunchKernelGGL(gather_blocks<Word16>, grid, dim3(kCopyLanes), 0, stream, pool, ids, staging, block_bytes, chunks);
+        else
+            hipLaunchKernelGGL(gather_blocks<Word8>, grid, dim3(kCopyLanes), 0, stream, pool, ids, staging, block_bytes, chunks);
+        check(hipGetLastError(), "launch gather_blocks");
+    }
+
+    void launch_scatter(Stream stream, uint8_t* pool, const uint32_t* ids, const uint8_t* staging, uint64_t block_bytes, uint32_t blocks) {
+        const uint32_t chunks = chunks_for(block_bytes);
+        const dim3 grid(chunks * blocks);
+        if (wide(pool, staging, block_bytes))
+            hipLaunchKernelGGL(scatter_blocks<Word16>, grid, dim3(kCopyLanes), 0, stream, pool, ids, staging, block_bytes, chunks);
+        else
+            hipLaunchKernelGGL(scatter_blocks<Word8>, grid, dim3(kCopyLanes), 0, stream, pool, ids, staging, block_bytes, chunks);
+        check(hipGetLastError(), "launch scatter_blocks");
+    }
+
+   private:
+    static uint32_t chunks_for(uint64_t block_bytes) { return uint32_t((block_bytes + kCopyChunk - 1) / kCopyChunk); }
+
+    static bool wide(const void* a, const void* b, uint64_t block_bytes) {
+        return ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) | block_bytes) & 15) == 0;
+    }
+
+    static void check(hipError_t status, const char* call) {
+        if (status != hipSuccess) throw std::runtime_error(std::string(call) + ": " + hipGetErrorName(status) + ": " + hipGetErrorString(status));
+    }
+
+    int device_;
+};
+
+}  // namespace lt
+
+using Device = lt::HipDevice;
+
+#include "transfer_exports.h"
+
+static int host_only(const char* name) {
+    lt::last_error = std::string(name) + " exists only in the host flavour";
+    return LT_ERR_UNSUPPORTED;
+}
+
+LT_EXPORT int lt_host_stream(lt_engine*, void**) { return host_only("lt_host_stream"); }
+LT_EXPORT int lt_host_call(lt_engine*, void*, lt_host_kernel, void*) { return host_only("lt_host_call"); }
+LT_EXPORT int lt_host_set_paused(lt_engine*, int) { return host_only("lt_host_set_paused"); }
+LT_EXPORT int lt_host_set_copy_delay_us(lt_engine*, uint32_t) { return host_only("lt_host_set_copy_delay_us"); }
+LT_EXPORT int lt_host_set_pin_limit(lt_engine*, uint64_t) { return host_only("lt_host_set_pin_limit"); }
