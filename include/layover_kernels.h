@@ -1,0 +1,98 @@
+/*
+ * layover_kernels.h: C ABI of the KV data-path kernels for MI355X (gfx950).
+ *
+ * The reference runs these as Triton kernels called from Python; each entry point below
+ * replaces one of those call sites and keeps its argument meaning:
+ *   lk_fp8_quantize    layover/kernels/fp8.py:349-367 quantize_blocks (_quantize_kernel :241-270)
+ *   lk_fp8_dequantize  layover/kernels/fp8.py:370-384 dequantize_blocks (_dequantize_kernel :272-294)
+ *   lk_fp8_encode      layover/kernels/fp8.py:319-323 encode_bits_triton (_encode_kernel :296-299)
+ *   lk_fp8_decode      layover/kernels/fp8.py:326-329 decode_bits_triton (_decode_kernel :301-304)
+ *   lk_paged_decode    layover/kernels/triton_decode.py:131-179 kernel_launch/run_kernel
+ *                      (_paged_decode_kernel :39-119); the FP8-record KV format has no
+ *                      reference counterpart (the reference decodes BF16 and FP32 pools only).
+ *
+ * Conventions: plain device pointers and sizes; `stream` is a hipStream_t (a torch stream's
+ * cuda_stream; null means the legacy default stream). Every entry point only enqueues work
+ * and returns LK_OK, or returns LK_ERR_INVALID with nothing enqueued when the arguments do
+ * not describe a launch the kernels support (the message is in lk_last_error). Block ids and
+ * lengths are not read on the host: the caller has checked them (as the reference's trusted
+ * decode path does, triton_decode.py:248-261).
+ */
+#ifndef LAYOVER_KERNELS_H
+#define LAYOVER_KERNELS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LK_ABI_VERSION 1
+
+enum { LK_OK = 0, LK_ERR_INVALID = 1, LK_ERR_DEVICE = 2 };
+
+/* Element formats of q/out and of the KV pool. */
+enum {
+    LK_BF16 = 0,      /* bfloat16 */
+    LK_F32 = 1,       /* float32 */
+    LK_FP8_RECORD = 2 /* KV only: FP8 E4M3 records with per-group int16 shifts (see below) */
+};
+
+int lk_abi_version(void);
+const char* lk_last_error(void);
+
+/* Quantize blocks ids[0..count) of a BF16 pool into `count` records at the front of `stage`.
+ * A block is groups_per_block groups of group_elems consecutive BF16 values. Record i is
+ * group_elems*groups_per_block E4M3 bytes (block ids[i], in pool order) followed by one
+ * little-endian int16 shift per group: record_bytes = block_elems + 2*groups_per_block. Each
+ * group is divided by 2**shift, shift = (largest finite nonzero BF16 exponent) - 134, or 0
+ * for a group without one, and rounded to nearest even; see fp8.py:1-31 for the special
+ * values. Bytes of `stage` past count*record_bytes are untouched. */
+int lk_fp8_quantize(const void* pool, const int32_t* ids, uint32_t count, void* stage, uint64_t group_elems,
+                    uint32_t groups_per_block, void* stream);
+
+/* The inverse: records 0..count) of `stage` decoded into pool blocks ids[0..count). */
+int lk_fp8_dequantize(const void* stage, const int32_t* ids, uint32_t count, void* pool, uint64_t group_elems,
+                      uint32_t groups_per_block, void* stream);
+
+/* Elementwise codec at one shift, for exhaustive checks: n BF16 bit patterns -> n E4M3 bytes,
+ * and n E4M3 bytes -> n BF16 bit patterns. */
+int lk_fp8_encode(const uint16_t* bits, uint8_t* out, uint64_t n, int32_t shift, void* stream);
+int lk_fp8_decode(const uint8_t* codes, uint16_t* out, uint64_t n, int32_t shift, void* stream);
+
+/* Shape of one paged decode launch. Pool layout [block, kind(K=0,V=1), layer, kv_head, slot,
+ * dim] (reference layover/kv/paged_cache.py:40-49); for LK_FP8_RECORD each block is one
+ * record as produced by lk_fp8_quantize with group_elems = slots*head_dim and
+ * groups_per_block = 2*layers*kv_heads, i.e. the same element order. */
+typedef struct {
+    uint32_t batch;
+    uint32_t query_heads;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t layers;
+    uint32_t slots;       /* tokens per block */
+    uint32_t layer;       /* the layer this launch reads */
+    uint32_t table_width; /* blocks per table row */
+    int32_t q_format;     /* LK_BF16 or LK_F32; out has the same format */
+    int32_t kv_format;    /* LK_BF16, LK_F32 or LK_FP8_RECORD */
+    float scale;          /* softmax scale, 1/sqrt(head_dim) in the reference */
+} lk_decode_shape;
+
+/* Bytes of device workspace lk_paged_decode needs for this shape (split-K partial results).
+ * Depends only on the shape, never on lengths, so it can be sized once per batch layout. */
+uint64_t lk_paged_decode_workspace(const lk_decode_shape* shape);
+
+/* One decode step of one layer: out[b, h] = softmax(q[b,h] . K^T * scale) V over the first
+ * lengths[b] tokens of row b of `table` (int32 [batch, table_width]), where query head h
+ * reads KV head h / (query_heads / kv_heads). q and out are [batch, query_heads, head_dim]
+ * contiguous. Tokens at or past lengths[b] never contribute, whatever their slots hold.
+ * Accumulation is FP32; out is rounded to nearest even. Requires 1 <= lengths[b] <=
+ * table_width*slots and every id in range, which the caller has checked. */
+int lk_paged_decode(const lk_decode_shape* shape, const void* q, const void* pool, const int32_t* table,
+                    const int32_t* lengths, void* out, void* workspace, uint64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LAYOVER_KERNELS_H */

@@ -1,0 +1,221 @@
+// FP8 E4M3 records of KV blocks on gfx950: the fused gather+quantize and dequantize+scatter
+// kernels behind lk_fp8_quantize / lk_fp8_dequantize, and the elementwise codec.
+//
+// Arithmetic: the reference's integer codec on BF16 bit patterns (layover/kernels/fp8.py:
+// 86-137), so every byte and every restored BF16 pattern is identical to its output by
+// construction, including the cases a hardware float convert treats differently (BF16
+// subnormals -> signed zero, infinity and overflow -> sign|0x7F, decode saturating at
+// 0x7F7F and flushing below BF16's smallest normal).
+//
+// Layout of work: one wave64 per group. A Qwen3-4B group (16 slots x 128 dims = 2048 values,
+// 4 KiB of BF16) is 4 loads of 16 bytes per lane, each wave instruction reading 1 KiB
+// contiguous; the shift is a wave max-reduction of the masked exponents; the 2 KiB of codes
+// go out as 4 stores of 8 bytes per lane (512 bytes contiguous per instruction). Other group
+// sizes take a strided element loop. The kernels are HBM-bound: per Qwen3-4B block, quantize
+// reads 2,359,296 bytes and writes 1,180,800; dequantize the reverse.
+#ifndef LAYOVER_AMD_FP8_CODEC_H
+#define LAYOVER_AMD_FP8_CODEC_H
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace lk {
+
+constexpr uint32_t kWave = 64;
+constexpr uint32_t kCodecWaves = 4;  // waves per workgroup
+
+// fp8.py:95-116: BF16 bits / 2**shift -> E4M3 byte, rounding the significand to nearest even.
+__device__ __forceinline__ uint32_t encode_e4m3(uint32_t bits, int32_t shift) {
+    const uint32_t sign = (bits >> 15) & 1u;
+    const int32_t raw = int32_t((bits >> 7) & 0xFFu);
+    const int32_t biased = raw - 127 - shift + 7;
+    const uint32_t significand = (bits & 0x7Fu) | 0x80u;
+    int32_t right = 4 + (biased < 1 ? 1 - biased : 0);
+    right = right > 15 ? 15 : right;
+    uint32_t kept = significand >> right;
+    const uint32_t remainder = significand & ((1u << right) - 1u);
+    const uint32_t half = 1u << (right - 1);
+    kept += (remainder > half || (remainder == half && (kept & 1u))) ? 1u : 0u;
+    int32_t magnitude = biased > 0 ? ((biased - 1) << 3) + int32_t(kept) : int32_t(kept);
+    magnitude = magnitude > 0x7E ? 0x7F : magnitude;
+    magnitude = raw == 0 ? 0 : magnitude;
+    magnitude = raw == 0xFF ? 0x7F : magnitude;
+    return (sign << 7) | uint32_t(magnitude);
+}
+
+// fp8.py:119-137: E4M3 byte * 2**shift -> BF16 bits.
+__device__ __forceinline__ uint32_t decode_e4m3(uint32_t code, int32_t shift) {
+    const uint32_t sign = (code >> 7) & 1u;
+    const uint32_t magnitude = code & 0x7Fu;
+    const int32_t raw = int32_t(magnitude >> 3);
+    uint32_t fraction = magnitude & 7u;
+    const int32_t top = fraction >= 4 ? 2 : (fraction >= 2 ? 1 : 0);
+    const int32_t exponent = raw > 0 ? raw - 7 : top - 9;
+    fraction = raw > 0 ? fraction : ((fraction << (3 - top)) & 7u);
+    const int32_t biased = exponent + shift + 127;
+    uint32_t out = (uint32_t(biased) << 7) | (fraction << 4);
+    out = biased >= 0xFF ? 0x7F7Fu : out;
+    out = biased <= 0 ? 0u : out;
+    out = magnitude == 0 ? 0u : out;
+    out |= sign << 15;
+    return magnitude == 0x7F ? 0x7FC0u : out;
+}
+
+// Exponent field shifted up one step, with infinity/NaN mapped to 0, so a plain unsigned max
+// over a group finds the largest finite exponent (+1; zero and subnormals give 1).
+__device__ __forceinline__ uint32_t exponent_key(uint32_t bits) {
+    return (((bits & 0x7F80u) + 0x80u) & 0x7FFFu) >> 7;
+}
+
+__device__ __forceinline__ int32_t shift_from_key(uint32_t largest_key) {
+    const int32_t largest = int32_t(largest_key) - 1;  // back to the raw exponent
+    return largest > 0 ? largest - 127 - 7 : 0;
+}
+
+__device__ __forceinline__ uint32_t wave_max(uint32_t value) {
+#pragma unroll
+    for (int mask = 32; mask >= 1; mask >>= 1) {
+        const uint32_t other = __shfl_xor(value, mask, kWave);
+        value = other > value ? other : value;
+    }
+    return value;
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Qwen3-shaped groups: 2048 values, everything 16-byte aligned.
+constexpr uint32_t kFastGroup = 2048;
+
+__global__ __launch_bounds__(kWave* kCodecWaves) void quantize_groups_2048(const uint16_t* __restrict__ pool,
+                                                                         const int32_t* __restrict__ ids, uint8_t* __restrict__ stage,
+                                                                         uint32_t count, uint32_t groups_per_block) {
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint64_t group = uint64_t(blockIdx.x) * kCodecWaves + threadIdx.x / kWave;
+    if (group >= uint64_t(count) * groups_per_block) return;
+    const uint32_t index = uint32_t(group / groups_per_block);
+    const uint32_t g = uint32_t(group % groups_per_block);
+    const uint64_t block_elems = uint64_t(kFastGroup) * groups_per_block;
+    const uint64_t record = block_elems + 2ull * groups_per_block;
+    const u32x4* source = reinterpret_cast<const u32x4*>(pool + uint64_t(ids[index]) * block_elems + uint64_t(g) * kFastGroup);
+
+    u32x4 words[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) words[j] = __builtin_nontemporal_load(source + j * kWave + lane);
+
+    uint32_t key = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t lo = exponent_key(words[j][w] & 0xFFFFu), hi = exponent_key(words[j][w] >> 16);
+            key = lo > key ? lo : key;
+            key = hi > key ? hi : key;
+        }
+    const int32_t shift = shift_from_key(wave_max(key));
+
+    uint8_t* out = stage + uint64_t(index) * record;
+    u32x2* codes = reinterpret_cast<u32x2*>(out + uint64_t(g) * kFastGroup);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        uint32_t packed[2];
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const uint32_t a = words[j][2 * half], b = words[j][2 * half + 1];
+            packed[half] = encode_e4m3(a & 0xFFFFu, shift) | (encode_e4m3(a >> 16, shift) << 8) |
+                           (encode_e4m3(b & 0xFFFFu, shift) << 16) | (encode_e4m3(b >> 16, shift) << 24);
+        }
+        codes[j * kWave + lane] = u32x2{packed[0], packed[1]};
+    }
+    if (lane == 0) {
+        const int16_t stored = int16_t(shift);
+        *reinterpret_cast<int16_t*>(out + block_elems + 2ull * g) = stored;
+    }
+}
+
+__global__ __launch_bounds__(kWave* kCodecWaves) void dequantize_groups_2048(const uint8_t* __restrict__ stage,
+                                                                           const int32_t* __restrict__ ids, uint16_t* __restrict__ pool,
+                                                                           uint32_t count, uint32_t groups_per_block) {
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint64_t group = uint64_t(blockIdx.x) * kCodecWaves + threadIdx.x / kWave;
+    if (group >= uint64_t(count) * groups_per_block) return;
+    const uint32_t index = uint32_t(group / groups_per_block);
+    const uint32_t g = uint32_t(group % groups_per_block);
+    const uint64_t block_elems = uint64_t(kFastGroup) * groups_per_block;
+    const uint64_t record = block_elems + 2ull * groups_per_block;
+    const uint8_t* in = stage + uint64_t(index) * record;
+    const int32_t shift = *reinterpret_cast<const int16_t*>(in + block_elems + 2ull * g);
+    const u32x2* codes = reinterpret_cast<const u32x2*>(in + uint64_t(g) * kFastGroup);
+    u32x4* target = reinterpret_cast<u32x4*>(pool + uint64_t(ids[index]) * block_elems + uint64_t(g) * kFastGroup);
+
+    u32x2 bytes[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bytes[j] = __builtin_nontemporal_load(codes + j * kWave + lane);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        u32x4 out;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t word = bytes[j][w / 2] >> (16 * (w % 2));
+            out[w] = decode_e4m3(word & 0xFFu, shift) | (decode_e4m3((word >> 8) & 0xFFu, shift) << 16);
+        }
+        target[j * kWave + lane] = out;
+    }
+}
+
+// Any group size and alignment: element-strided loops, one wave per group.
+__global__ __launch_bounds__(kWave* kCodecWaves) void quantize_groups_any(const uint16_t* __restrict__ pool, const int32_t* __restrict__ ids,
+                                                                        uint8_t* __restrict__ stage, uint32_t count,
+                                                                        uint64_t group_elems, uint32_t groups_per_block) {
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint64_t group = uint64_t(blockIdx.x) * kCodecWaves + threadIdx.x / kWave;
+    if (group >= uint64_t(count) * groups_per_block) return;
+    const uint32_t index = uint32_t(group / groups_per_block);
+    const uint32_t g = uint32_t(group % groups_per_block);
+    const uint64_t block_elems = group_elems * groups_per_block;
+    const uint64_t record = block_elems + 2ull * groups_per_block;
+    const uint16_t* source = pool + uint64_t(ids[index]) * block_elems + uint64_t(g) * group_elems;
+    uint32_t key = 0;
+    for (uint64_t e = lane; e < group_elems; e += kWave) {
+        const uint32_t k = exponent_key(source[e]);
+        key = k > key ? k : key;
+    }
+    const int32_t shift = shift_from_key(wave_max(key));
+    uint8_t* out = stage + uint64_t(index) * record;
+    for (uint64_t e = lane; e < group_elems; e += kWave) out[uint64_t(g) * group_elems + e] = uint8_t(encode_e4m3(source[e], shift));
+    if (lane == 0) {
+        const uint16_t stored = uint16_t(int16_t(shift));
+        out[block_elems + 2ull * g] = uint8_t(stored & 0xFFu);
+        out[block_elems + 2ull * g + 1] = uint8_t(stored >> 8);
+    }
+}
+
+__global__ __launch_bounds__(kWave* kCodecWaves) void dequantize_groups_any(const uint8_t* __restrict__ stage,
+                                                                          const int32_t* __restrict__ ids, uint16_t* __restrict__ pool,
+                                                                          uint32_t count, uint64_t group_elems, uint32_t groups_per_block) {
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint64_t group = uint64_t(blockIdx.x) * kCodecWaves + threadIdx.x / kWave;
+    if (group >= uint64_t(count) * groups_per_block) return;
+    const uint32_t index = uint32_t(group / groups_per_block);
+    const uint32_t g = uint32_t(group % groups_per_block);
+    const uint64_t block_elems = group_elems * groups_per_block;
+    const uint64_t record = block_elems + 2ull * groups_per_block;
+    const uint8_t* in = stage + uint64_t(index) * record;
+    const int32_t shift = int16_t(uint16_t(in[block_elems + 2ull * g]) | uint16_t(in[block_elems + 2ull * g + 1] << 8));
+    uint16_t* target = pool + uint64_t(ids[index]) * block_elems + uint64_t(g) * group_elems;
+    for (uint64_t e = lane; e < group_elems; e += kWave) target[e] = uint16_t(decode_e4m3(in[uint64_t(g) * group_elems + e], shift));
+}
+
+__global__ void encode_elements(const uint16_t* __restrict__ bits, uint8_t* __restrict__ out, uint64_t n, int32_t shift) {
+    const uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = uint8_t(encode_e4m3(bits[i], shift));
+}
+
+__global__ void decode_elements(const uint8_t* __restrict__ codes, uint16_t* __restrict__ out, uint64_t n, int32_t shift) {
+    const uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = uint16_t(decode_e4m3(codes[i], shift));
+}
+
+}  // namespace lk
+
+#endif  // LAYOVER_AMD_FP8_CODEC_H

@@ -1,0 +1,268 @@
+// The C ABI of include/layover_kernels.h: host-side argument checks, launch geometry and
+// template dispatch for the FP8 record kernels (fp8_codec.h) and paged decode attention
+// (decode_attention.h). Every entry point only enqueues; nothing here reads device memory.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdlib.h>
+
+#include <stdexcept>
+#include <string>
+
+#include "decode_attention.h"
+#include "fp8_codec.h"
+#include "layover_kernels.h"
+
+namespace lk {
+
+thread_local std::string last_error;
+
+struct Invalid : std::invalid_argument {
+    using std::invalid_argument::invalid_argument;
+};
+
+template <class Fn>
+int guarded(Fn&& fn) {
+    try {
+        fn();
+        const hipError_t status = hipGetLastError();
+        if (status != hipSuccess) {
+            last_error = std::string("kernel launch failed: ") + hipGetErrorName(status) + ": " + hipGetErrorString(status);
+            return LK_ERR_DEVICE;
+        }
+        return LK_OK;
+    } catch (const std::invalid_argument& error) {
+        last_error = error.what();
+        return LK_ERR_INVALID;
+    } catch (const std::exception& error) {
+        last_error = error.what();
+        return LK_ERR_DEVICE;
+    }
+}
+
+inline bool aligned(const void* pointer, uintptr_t to) { return (reinterpret_cast<uintptr_t>(pointer) % to) == 0; }
+
+inline void require(bool condition, const char* message) {
+    if (!condition) throw Invalid(message);
+}
+
+inline uint32_t grid_for_groups(uint64_t groups) {
+    const uint64_t workgroups = (groups + kCodecWaves - 1) / kCodecWaves;
+    require(workgroups <= 0x7FFFFFFFull, "too many groups for one launch");
+    return uint32_t(workgroups);
+}
+
+void check_records(const void* pool, const int32_t* ids, uint32_t count, const void* stage, uint64_t group_elems,
+                   uint32_t groups_per_block) {
+    require(pool != nullptr && stage != nullptr && (ids != nullptr || count == 0), "null pool, ids or stage");
+    require(group_elems > 0 && groups_per_block > 0, "group_elems and groups_per_block must be positive");
+    require(aligned(pool, 2), "the BF16 pool must be 2-byte aligned");
+}
+
+bool fast_records(const void* pool, const void* stage, uint64_t group_elems, uint32_t groups_per_block) {
+    const uint64_t record = group_elems * groups_per_block + 2ull * groups_per_block;
+    return group_elems == kFastGroup && aligned(pool, 16) && aligned(stage, 16) && record % 16 == 0;
+}
+
+// Decode launch geometry: blocks per split (bps) and splits per sequence, from the shape only.
+// Enough workgroups to keep all 256 CUs busy at the widest table (about 16 per CU at full
+// lengths), but splits of at least 16 blocks so each wave streams several tiles.
+struct Geometry {
+    uint32_t bps;
+    uint32_t splits;
+    bool fast;
+};
+
+uint32_t env_bps() {
+    static const uint32_t value = [] {
+        const char* text = getenv("LAYOVER_DECODE_BPS");
+        return text ? uint32_t(strtoul(text, nullptr, 10)) : 0u;
+    }();
+    return value;
+}
+
+uint64_t pool_block_bytes(const lk_decode_shape& s) {
+    const uint64_t elems = 2ull * s.layers * s.kv_heads * s.slots * s.head_dim;
+    if (s.kv_format == LK_FP8_RECORD) return elems + 2ull * 2 * s.layers * s.kv_heads;
+    return elems * (s.kv_format == LK_F32 ? 4 : 2);
+}
+
+// The fast kernel needs the Qwen3 tile shape, a supported GQA ratio, and 16-byte aligned
+// tiles (pool base and block stride); anything else runs the generic kernel.
+bool fast_decode(const lk_decode_shape& s, const void* pool) {
+    const uint32_t groups = s.query_heads / s.kv_heads;
+    return s.slots == kSlots && s.head_dim == kDim && (groups == 1 || groups == 2 || groups == 4 || groups == 8) &&
+           aligned(pool, 16) && pool_block_bytes(s) % 16 == 0;
+}
+
+Geometry geometry(const lk_decode_shape& s, const void* pool = nullptr) {
+    Geometry g{};
+    g.fast = pool != nullptr && fast_decode(s, pool);
+    // Work units counted per KV head for both kernels, so the split count (and with it the
+    // workspace size) does not depend on which kernel runs.
+    const uint64_t units = uint64_t(s.batch) * s.kv_heads;
+    uint32_t bps = env_bps();
+    if (bps == 0) {
+        const uint64_t target = 4096;
+        const uint64_t wanted = (units * s.table_width + target - 1) / target;
+        bps = 16;
+        while (bps < wanted && bps < 256) bps *= 2;
+    }
+    g.bps = bps;
+    g.splits = (s.table_width + bps - 1) / bps;
+    return g;
+}
+
+void check_shape(const lk_decode_shape& s) {
+    require(s.batch > 0 && s.query_heads > 0 && s.kv_heads > 0 && s.head_dim > 0 && s.layers > 0 && s.slots > 0 &&
+                s.table_width > 0,
+            "every decode dimension must be positive");
+    require(s.query_heads % s.kv_heads == 0, "query heads must be a multiple of KV heads");
+    require(s.layer < s.layers, "layer out of range");
+    require(s.q_format == LK_BF16 || s.q_format == LK_F32, "q must be LK_BF16 or LK_F32");
+    require(s.kv_format == LK_BF16 || s.kv_format == LK_F32 || s.kv_format == LK_FP8_RECORD, "unknown KV format");
+    require(s.head_dim <= kMaxGenericDim || (s.slots == kSlots && s.head_dim == kDim), "head_dim above 256 is not supported");
+    require(s.slots <= 1024, "more than 1024 slots per block is not supported");
+}
+
+uint64_t workspace_bytes(const lk_decode_shape& s) {
+    const Geometry g = geometry(s);
+    return uint64_t(s.batch) * s.query_heads * g.splits * (uint64_t(s.head_dim) + 2) * sizeof(float);
+}
+
+template <int KV, int QF>
+void launch_fast(const DecodeArgs& a, uint32_t grid, hipStream_t stream) {
+    switch (a.groups) {
+        case 1: hipLaunchKernelGGL((decode_split_fast<KV, QF, 1>), dim3(grid), dim3(kWave * kDecodeWaves), 0, stream, a); break;
+        case 2: hipLaunchKernelGGL((decode_split_fast<KV, QF, 2>), dim3(grid), dim3(kWave * kDecodeWaves), 0, stream, a); break;
+        case 4: hipLaunchKernelGGL((decode_split_fast<KV, QF, 4>), dim3(grid), dim3(kWave * kDecodeWaves), 0, stream, a); break;
+        default: hipLaunchKernelGGL((decode_split_fast<KV, QF, 8>), dim3(grid), dim3(kWave * kDecodeWaves), 0, stream, a); break;
+    }
+}
+
+template <int QF>
+void launch_decode(const DecodeArgs& a, const Geometry& g, int kv, void* out, hipStream_t stream) {
+    if (g.fast) {
+        const uint64_t grid = uint64_t(a.batch) * a.kv_heads * g.splits;
+        require(grid <= 0x7FFFFFFFull, "decode grid too large");
+        if (kv == LK_BF16) launch_fast<LK_BF16, QF>(a, uint32_t(grid), stream);
+        else if (kv == LK_F32) launch_fast<LK_F32, QF>(a, uint32_t(grid), stream);
+        else launch_fast<LK_FP8_RECORD, QF>(a, uint32_t(grid), stream);
+    } else {
+        const uint64_t grid = uint64_t(a.batch) * a.query_heads * g.splits;
+        require(grid <= 0x7FFFFFFFull, "decode grid too large");
+        if (kv == LK_BF16) hipLaunchKernelGGL((decode_split_generic<LK_BF16, QF>), dim3(uint32_t(grid)), dim3(kWave), 0, stream, a);
+        else if (kv == LK_F32) hipLaunchKernelGGL((decode_split_generic<LK_F32, QF>), dim3(uint32_t(grid)), dim3(kWave), 0, stream, a);
+        else hipLaunchKernelGGL((decode_split_generic<LK_FP8_RECORD, QF>), dim3(uint32_t(grid)), dim3(kWave), 0, stream, a);
+    }
+    hipLaunchKernelGGL((decode_combine<QF>), dim3(a.batch * a.query_heads), dim3(kWave), 0, stream, a, out);
+}
+
+}  // namespace lk
+
+#define LK_EXPORT extern "C" __attribute__((visibility("default")))
+
+LK_EXPORT int lk_abi_version(void) { return LK_ABI_VERSION; }
+LK_EXPORT const char* lk_last_error(void) { return lk::last_error.c_str(); }
+
+LK_EXPORT int lk_fp8_quantize(const void* pool, const int32_t* ids, uint32_t count, void* stage, uint64_t group_elems,
+                              uint32_t groups_per_block, void* stream) {
+    return lk::guarded([&] {
+        lk::check_records(pool, ids, count, stage, group_elems, groups_per_block);
+        if (count == 0) return;
+        const uint64_t groups = uint64_t(count) * groups_per_block;
+        const uint32_t grid = lk::grid_for_groups(groups);
+        const dim3 block(lk::kWave * lk::kCodecWaves);
+        auto s = static_cast<hipStream_t>(stream);
+        if (lk::fast_records(pool, stage, group_elems, groups_per_block))
+            hipLaunchKernelGGL(lk::quantize_groups_2048, dim3(grid), block, 0, s, static_cast<const uint16_t*>(pool), ids,
+                               static_cast<uint8_t*>(stage), count, groups_per_block);
+        else
+            hipLaunchKernelGGL(lk::quantize_groups_any, dim3(grid), block, 0, s, static_cast<const uint16_t*>(pool), ids,
+                               static_cast<uint8_t*>(stage), count, group_elems, groups_per_block);
+    });
+}
+
+LK_EXPORT int lk_fp8_dequantize(const void* stage, const int32_t* ids, uint32_t count, void* pool, uint64_t group_elems,
+                                uint32_t groups_per_block, void* stream) {
+    return lk::guarded([&] {
+        lk::check_records(pool, ids, count, stage, group_elems, groups_per_block);
+        if (count == 0) return;
+        const uint64_t groups = uint64_t(count) * groups_per_block;
+        const uint32_t grid = lk::grid_for_groups(groups);
+        const dim3 block(lk::kWave * lk::kCodecWaves);
+        auto s = static_cast<hipStream_t>(stream);
+        if (lk::fast_records(pool, stage, group_elems, groups_per_block))
+            hipLaunchKernelGGL(lk::dequantize_groups_2048, dim3(grid), block, 0, s, static_cast<const uint8_t*>(stage), ids,
+                               static_cast<uint16_t*>(pool), count, groups_per_block);
+        else
+            hipLaunchKernelGGL(lk::dequantize_groups_any, dim3(grid), block, 0, s, static_cast<const uint8_t*>(stage), ids,
+                               static_cast<uint16_t*>(pool), count, group_elems, groups_per_block);
+    });
+}
+
+LK_EXPORT int lk_fp8_encode(const uint16_t* bits, uint8_t* out, uint64_t n, int32_t shift, void* stream) {
+    return lk::guarded([&] {
+        lk::require(bits != nullptr && out != nullptr, "null input or output");
+        if (n == 0) return;
+        const uint64_t grid = (n + 255) / 256;
+        lk::require(grid <= 0x7FFFFFFFull, "too many elements for one launch");
+        hipLaunchKernelGGL(lk::encode_elements, dim3(uint32_t(grid)), dim3(256), 0, static_cast<hipStream_t>(stream), bits, out, n, shift);
+    });
+}
+
+LK_EXPORT int lk_fp8_decode(const uint8_t* codes, uint16_t* out, uint64_t n, int32_t shift, void* stream) {
+    return lk::guarded([&] {
+        lk::require(codes != nullptr && out != nullptr, "null input or output");
+        if (n == 0) return;
+        const uint64_t grid = (n + 255) / 256;
+        lk::require(grid <= 0x7FFFFFFFull, "too many elements for one launch");
+        hipLaunchKernelGGL(lk::decode_elements, dim3(uint32_t(grid)), dim3(256), 0, static_cast<hipStream_t>(stream), codes, out, n, shift);
+    });
+}
+
+LK_EXPORT uint64_t lk_paged_decode_workspace(const lk_decode_shape* shape) {
+    if (shape == nullptr) return 0;
+    try {
+        lk::check_shape(*shape);
+    } catch (const std::exception&) {
+        return 0;
+    }
+    return lk::workspace_bytes(*shape);
+}
+
+LK_EXPORT int lk_paged_decode(const lk_decode_shape* shape, const void* q, const void* pool, const int32_t* table,
+                              const int32_t* lengths, void* out, void* workspace, uint64_t workspace_bytes, void* stream) {
+    return lk::guarded([&] {
+        lk::require(shape != nullptr, "null shape");
+        const lk_decode_shape& s = *shape;
+        lk::check_shape(s);
+        lk::require(q && pool && table && lengths && out && workspace, "null q, pool, table, lengths, out or workspace");
+        lk::require(workspace_bytes >= lk::workspace_bytes(s), "workspace smaller than lk_paged_decode_workspace");
+        lk::require(lk::aligned(workspace, 4), "workspace must be 4-byte aligned");
+        const lk::Geometry g = lk::geometry(s, pool);
+        lk::DecodeArgs a{};
+        a.q = q;
+        a.pool = static_cast<const uint8_t*>(pool);
+        a.table = table;
+        a.lengths = lengths;
+        a.partial_acc = static_cast<float*>(workspace);
+        a.partial_ml = a.partial_acc + uint64_t(s.batch) * s.query_heads * g.splits * s.head_dim;
+        a.batch = s.batch;
+        a.query_heads = s.query_heads;
+        a.kv_heads = s.kv_heads;
+        a.head_dim = s.head_dim;
+        a.layers = s.layers;
+        a.slots = s.slots;
+        a.layer = s.layer;
+        a.table_width = s.table_width;
+        a.groups = s.query_heads / s.kv_heads;
+        a.splits = g.splits;
+        a.bps = g.bps;
+        a.block_bytes = lk::pool_block_bytes(s);
+        a.scale_log2 = s.scale * lk::kLog2e;
+        lk::require(lk::aligned(pool, s.kv_format == LK_F32 ? 4 : (s.kv_format == LK_BF16 ? 2 : 1)), "misaligned pool");
+        auto st = static_cast<hipStream_t>(stream);
+        if (s.q_format == LK_BF16) lk::launch_decode<LK_BF16>(a, g, s.kv_format, out, st);
+        else lk::launch_decode<LK_F32>(a, g, s.kv_format, out, st);
+    });
+}

@@ -1,0 +1,170 @@
+"""Paged GQA decode attention as a gfx950 HIP kernel.
+
+Drop-in for the reference's layover/kernels/triton_decode.py call sites:
+paged_decode_attention_hip / paged_decode_attention_hip_trusted take the arguments of
+paged_decode_attention_triton / _trusted (triton_decode.py:235-261) and refuse the same bad
+inputs before anything is launched (validate_shapes / validate, triton_decode.py:182-232).
+The kernel reads K and V through the block table straight from the pool, with an online
+softmax in FP32, split-K over the context and a combine pass (layover_amd/csrc/
+decode_attention.h), through liblayover_kernels.so.
+
+Pools: BF16 or FP32 tensors shaped [block, 2, layers, kv_heads, slots, dim]
+(paged_cache.py:40-49), or an Fp8KVPool of FP8 records in the format of
+layover_amd.kernels.fp8 (the reference has no FP8 decode; its record format is reused).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from layover_amd.kernels import _lib
+from layover_amd.kernels.fp8 import Fp8Layout
+
+KV_KINDS = 2
+KV_DTYPES = (torch.bfloat16, torch.float32)
+_FORMATS = {torch.bfloat16: _lib.LK_BF16, torch.float32: _lib.LK_F32}
+
+
+@dataclass
+class Fp8KVPool:
+    """A KV pool held as FP8 records: `records` is uint8 [blocks, record_bytes], each row the
+    record lk_fp8_quantize writes for one block of a [2, layers, kv_heads, slots, head_dim]
+    BF16 block."""
+
+    records: torch.Tensor
+    layers: int
+    kv_heads: int
+    slots: int
+    head_dim: int
+
+    @property
+    def layout(self) -> Fp8Layout:
+        return Fp8Layout(self.slots * self.head_dim, KV_KINDS * self.layers * self.kv_heads)
+
+    @property
+    def shape(self) -> tuple[int, ...]:
+        return (self.records.shape[0], KV_KINDS, self.layers, self.kv_heads, self.slots, self.head_dim)
+
+    @property
+    def device(self) -> torch.device:
+        return self.records.device
+
+    def dim(self) -> int:
+        return 6
+
+    def is_contiguous(self) -> bool:
+        return self.records.is_contiguous()
+
+    @classmethod
+    def empty(cls, blocks: int, layers: int, kv_heads: int, slots: int, head_dim: int, device) -> "Fp8KVPool":
+        layout = Fp8Layout(slots * head_dim, KV_KINDS * layers * kv_heads)
+        return cls(torch.zeros(blocks, layout.record_bytes, dtype=torch.uint8, device=device), layers, kv_heads, slots, head_dim)
+
+
+def _is_fp8(pool) -> bool:
+    return isinstance(pool, Fp8KVPool)
+
+
+def validate_shapes(q, pool, layer, block_table, lengths, kv_groups) -> None:
+    """Everything that can be checked without reading the GPU (triton_decode.py:182-215)."""
+    if q.dim() != 3 or pool.dim() != 6 or block_table.dim() != 2 or lengths.dim() != 1:
+        raise ValueError(f"bad ranks: q {tuple(q.shape)}, pool {tuple(pool.shape)}, table {tuple(block_table.shape)}, lengths {tuple(lengths.shape)}")
+    if not pool.is_contiguous():
+        raise ValueError("the pool must be contiguous: its strides are derived from its shape")
+    if _is_fp8(pool):
+        if pool.records.dtype != torch.uint8 or pool.records.dim() != 2 or pool.records.shape[1] != pool.layout.record_bytes:
+            raise ValueError("an FP8 pool is uint8 [blocks, record_bytes]")
+    elif pool.dtype not in KV_DTYPES:
+        raise ValueError(f"the pool is {pool.dtype}; the kernel takes {KV_DTYPES} or an Fp8KVPool")
+    if q.dtype not in KV_DTYPES:
+        raise ValueError(f"q is {q.dtype}; the kernel takes {KV_DTYPES}")
+    batch, query_heads, head_dim = q.shape
+    blocks, kinds, layers, kv_heads, slots, pool_dim = pool.shape
+    if kinds != KV_KINDS:
+        raise ValueError(f"pool has {kinds} kinds, expected K and V")
+    if head_dim != pool_dim:
+        raise ValueError(f"q head_dim {head_dim} differs from the pool's {pool_dim}")
+    if kv_groups < 1 or query_heads != kv_heads * kv_groups:
+        raise ValueError(f"{query_heads} query heads cannot share {kv_heads} KV heads in groups of {kv_groups}")
+    if not 0 <= layer < layers:
+        raise ValueError(f"layer {layer} out of range for {layers} layers")
+    if block_table.shape[0] != batch or lengths.shape[0] != batch:
+        raise ValueError(f"batch {batch} disagrees with table {tuple(block_table.shape)} and lengths {tuple(lengths.shape)}")
+    if block_table.shape[1] < 1:
+        raise ValueError("the block table has no columns")
+    devices = {q.device, pool.device, block_table.device, lengths.device}
+    if len(devices) != 1:
+        raise ValueError(f"tensors span devices {devices}")
+    if q.device.type != "cuda":
+        raise ValueError(f"tensors are on {q.device}: the HIP kernel runs on the GPU only")
+    if q.device.index != torch.cuda.current_device():
+        raise ValueError(f"tensors are on {q.device}, the current device is {torch.cuda.current_device()}")
+    if block_table.is_floating_point() or lengths.is_floating_point():
+        raise TypeError("the block table and lengths must be integers")
+    if head_dim > 256 and not (slots == 16 and head_dim == 128):
+        raise ValueError(f"head_dim {head_dim} is not supported (at most 256)")
+
+
+def validate(q, pool, layer, block_table, lengths, kv_groups) -> None:
+    """validate_shapes plus the bounds a kernel cannot check for itself, at the cost of one
+    device read (triton_decode.py:218-232)."""
+    validate_shapes(q, pool, layer, block_table, lengths, kv_groups)
+    slots, blocks = pool.shape[4], pool.shape[0]
+    bounds = torch.stack([*torch.aminmax(lengths.long()), *torch.aminmax(block_table.long())])
+    shortest, longest, lowest, highest = bounds.tolist()
+    if shortest < 1 or longest > block_table.shape[1] * slots:
+        raise ValueError(f"lengths in [{shortest}, {longest}] do not fit a table of {block_table.shape[1]} blocks")
+    if lowest < 0 or highest >= blocks:
+        raise ValueError(f"block ids in [{lowest}, {highest}] are outside a pool of {blocks} blocks")
+
+
+def decode_shape(q, pool, layer, block_table, kv_groups) -> _lib.DecodeShape:
+    batch, query_heads, head_dim = q.shape
+    _, _, layers, kv_heads, slots, _ = pool.shape
+    kv_format = _lib.LK_FP8_RECORD if _is_fp8(pool) else _FORMATS[pool.dtype]
+    return _lib.DecodeShape(batch, query_heads, kv_heads, head_dim, layers, slots, layer, block_table.shape[1],
+                            _FORMATS[q.dtype], kv_format, 1.0 / math.sqrt(head_dim))
+
+
+def workspace_bytes(shape: _lib.DecodeShape) -> int:
+    return int(_lib.load().lk_paged_decode_workspace(shape))
+
+
+def run_kernel(q, pool, layer, block_table, lengths, kv_groups, out, workspace=None) -> None:
+    """Launch without validating, on the current stream. q, table, lengths and out must be
+    contiguous, table and lengths int32."""
+    lib = _lib.load()
+    shape = decode_shape(q, pool, layer, block_table, kv_groups)
+    need = int(lib.lk_paged_decode_workspace(shape))
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=q.device)
+    storage = pool.records if _is_fp8(pool) else pool
+    _lib.check(
+        lib.lk_paged_decode(shape, q.data_ptr(), storage.data_ptr(), block_table.data_ptr(), lengths.data_ptr(), out.data_ptr(),
+                            workspace.data_ptr(), workspace.numel(), _lib.current_stream(q.device))
+    )
+
+
+def _launch(q, pool, layer, block_table, lengths, kv_groups) -> torch.Tensor:
+    q = q.contiguous()
+    block_table = block_table.to(torch.int32).contiguous()
+    lengths = lengths.to(torch.int32).contiguous()
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    run_kernel(q, pool, layer, block_table, lengths, kv_groups, out)
+    return out
+
+
+def paged_decode_attention_hip(q, pool, layer, block_table, lengths, kv_groups) -> torch.Tensor:
+    """Drop-in for paged_decode_attention_triton: validated, result in q's dtype and device."""
+    validate(q, pool, layer, block_table, lengths, kv_groups)
+    return _launch(q, pool, layer, block_table, lengths, kv_groups)
+
+
+def paged_decode_attention_hip_trusted(q, pool, layer, block_table, lengths, kv_groups) -> torch.Tensor:
+    """For tables whose lengths and ids the caller checked on the host (as
+    PagedKVCache.decode_batch does): reads nothing back from the GPU."""
+    validate_shapes(q, pool, layer, block_table, lengths, kv_groups)
+    return _launch(q, pool, layer, block_table, lengths, kv_groups)

@@ -1,0 +1,319 @@
+"""GPU parity of the HIP kernels against the CPU oracle, through the C ABI wrappers.
+
+FP8: bit-exact (every BF16 pattern x every shift the computed scale can produce, and whole
+records at the Qwen3-4B and micro shapes). Decode: within the north-star tolerance
+(2e-2 abs / 1e-2 rel at BF16) of the float64 oracle, and much tighter in practice: the
+asserted bound is the BF16 rounding of the exact answer plus a small FP32 allowance.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+QWEN = dict(layers=36, kv_heads=8, slots=16, head_dim=128)
+
+
+@pytest.fixture(scope="module")
+def fp8():
+    from layover_amd.kernels import fp8 as module
+
+    return module
+
+
+@pytest.fixture(scope="module")
+def hip_decode():
+    from layover_amd.kernels import hip_decode as module
+
+    return module
+
+
+def test_kernel_library_loads_into_torchs_hip_runtime():
+    from layover_amd.kernels import _lib
+    from layover_amd.kv.native import hip_runtimes_loaded, load_library
+
+    torch.zeros(1, device="cuda")
+    lib = _lib.load()
+    assert lib.lk_abi_version() == 1
+    assert load_library("hip").lt_flavor() == b"hip"
+    assert len(hip_runtimes_loaded()) == 1, hip_runtimes_loaded()
+
+
+# FP8 codec: every pattern at every shift.
+
+ALL_BF16 = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+ALL_FP8 = np.arange(256, dtype=np.uint32).astype(np.uint8)
+
+
+def test_encode_is_bit_exact_for_every_pattern_and_every_shift(fp8):
+    bits = torch.from_numpy(ALL_BF16.view(np.int16)).cuda().view(torch.uint16)
+    for shift in range(-133, 121):
+        got = fp8.encode_bits_hip(bits, shift).cpu().numpy()
+        expected = oracle.encode(ALL_BF16, shift)
+        assert np.array_equal(got, expected), f"shift {shift}: {np.flatnonzero(got != expected)[:8]}"
+
+
+def test_decode_is_bit_exact_for_every_code_and_every_shift(fp8):
+    codes = torch.from_numpy(ALL_FP8).cuda()
+    for shift in range(-140, 128):
+        got = fp8.decode_bits_hip(codes, shift).cpu().numpy()
+        assert np.array_equal(got, oracle.decode(ALL_FP8, shift)), f"shift {shift}"
+
+
+def make_pool(blocks, layers, kv_heads, slots, head_dim, seed=0, outliers=0.0):
+    rng = np.random.default_rng(seed)
+    values = rng.standard_normal((blocks, 2, layers, kv_heads, slots, head_dim), dtype=np.float32)
+    values *= np.exp(rng.standard_normal(values.shape, dtype=np.float32))
+    if outliers:
+        mask = rng.random(values.shape) < outliers
+        values[mask] = np.where(rng.random(mask.sum()) < 0.5, -40.0, 40.0)
+    return oracle.bf16_bits(values)
+
+
+@pytest.mark.parametrize(
+    "shape",
+    [dict(QWEN, blocks=24), dict(layers=2, kv_heads=2, slots=16, head_dim=24, blocks=9), dict(layers=1, kv_heads=1, slots=16, head_dim=128, blocks=5)],
+    ids=["qwen3_4b", "micro", "one_group_pow2"],
+)
+def test_records_are_bit_exact_and_restore_bit_exact(fp8, shape):
+    blocks = shape.pop("blocks")
+    bits = make_pool(blocks, **shape, seed=1, outliers=0.001)
+    # Special values in one block: zeros, subnormals, infinities, NaN, the largest finite.
+    special = bits.reshape(blocks, -1)
+    special[1, :8] = [0x0000, 0x8000, 0x0001, 0x807F, 0x7F80, 0xFF80, 0x7FC1, 0x7F7F]
+    layout = fp8.Fp8Layout(shape["slots"] * shape["head_dim"], 2 * shape["layers"] * shape["kv_heads"])
+    ids = np.random.default_rng(2).permutation(blocks)[: blocks - 2].astype(np.int32)
+    expected = oracle.quantize_records(bits, ids, layout.group_elems, layout.groups_per_block)
+
+    pool = torch.from_numpy(bits.view(np.int16)).cuda().view(torch.bfloat16)
+    stage = torch.full((expected.size + 64,), 0xAB, dtype=torch.uint8, device="cuda")
+    fp8.quantize_blocks(pool, torch.from_numpy(ids).cuda(), stage, layout)
+    got = stage.cpu().numpy()
+    assert np.array_equal(got[: expected.size], expected)
+    assert (got[expected.size :] == 0xAB).all()
+
+    target_ids = np.random.default_rng(3).permutation(blocks)[: len(ids)].astype(np.int32)
+    restored = torch.zeros_like(pool)
+    fp8.dequantize_blocks(stage, torch.from_numpy(target_ids).cuda(), restored, layout)
+    reference = np.zeros_like(bits)
+    oracle.dequantize_records(expected, target_ids, reference, layout.group_elems, layout.groups_per_block)
+    assert np.array_equal(restored.view(torch.int16).cpu().numpy().view(np.uint16), reference)
+
+
+def test_records_address_past_4_gib(fp8):
+    layout = fp8.Fp8Layout(2048, 576)
+    block_bytes = 2 * layout.block_elems
+    blocks = (5 << 30) // block_bytes + 2
+    pool = torch.zeros(blocks, layout.block_elems, dtype=torch.bfloat16, device="cuda")
+    source, target = blocks - 1, blocks - 2
+    values = make_pool(1, 36, 8, 16, 128, seed=4).reshape(1, -1)
+    pool[source] = torch.from_numpy(values.view(np.int16)).cuda().view(torch.bfloat16)[0]
+    stage = torch.zeros(layout.record_bytes, dtype=torch.uint8, device="cuda")
+    fp8.quantize_blocks(pool, torch.tensor([source], dtype=torch.int32, device="cuda"), stage, layout)
+    expected = oracle.quantize_records(values, [0], layout.group_elems, layout.groups_per_block)
+    assert np.array_equal(stage.cpu().numpy(), expected)
+    fp8.dequantize_blocks(stage, torch.tensor([target], dtype=torch.int32, device="cuda"), pool, layout)
+    reference = np.zeros_like(values)
+    oracle.dequantize_records(expected, [0], reference, layout.group_elems, layout.groups_per_block)
+    assert np.array_equal(pool[target].view(torch.int16).cpu().numpy().view(np.uint16), reference[0])
+    del pool
+    torch.cuda.empty_cache()
+
+
+def test_a_non_bf16_pool_is_refused(fp8):
+    layout = fp8.Fp8Layout(384, 8)
+    pool = torch.zeros(2, layout.block_elems, dtype=torch.float32, device="cuda")
+    with pytest.raises(ValueError):
+        fp8.quantize_blocks(pool, torch.zeros(1, dtype=torch.int32, device="cuda"), torch.zeros(layout.record_bytes, dtype=torch.uint8, device="cuda"), layout)
+
+
+# Paged decode.
+
+
+def decode_case(lengths, layers, kv_heads, slots, head_dim, groups, seed=0, pool_blocks=None, gain=1.0):
+    rng = np.random.default_rng(seed)
+    width = max(-(-n // slots) for n in lengths)
+    blocks = pool_blocks or len(lengths) * width + 3
+    pool = oracle.bf16_bits(rng.standard_normal((blocks, 2, layers, kv_heads, slots, head_dim), dtype=np.float32))
+    if pool_blocks:
+        table = np.stack([rng.choice(blocks, width, replace=False) for _ in lengths]).astype(np.int32)
+    else:
+        table = rng.permutation(blocks)[: len(lengths) * width].reshape(len(lengths), width).astype(np.int32)
+    q = oracle.bf16_bits((gain * rng.standard_normal((len(lengths), kv_heads * groups, head_dim))).astype(np.float32))
+    return q, pool, table, np.array(lengths, dtype=np.int32)
+
+
+def to_gpu_bf16(bits):
+    return torch.from_numpy(bits.view(np.int16)).cuda().view(torch.bfloat16)
+
+
+def assert_close_to_oracle(out, expected, what=""):
+    got = out.double().cpu().numpy()
+    # BF16 rounding of the exact answer (2^-8 relative) plus an FP32 accumulation allowance;
+    # far inside the north-star 2e-2 abs / 1e-2 rel.
+    allowed = np.abs(expected) * 2.0**-8 + 1e-3
+    error = np.abs(got - expected)
+    assert np.isfinite(got).all(), what
+    assert (error <= allowed).all(), f"{what}: max error {error.max():.3g} at {np.unravel_index(error.argmax(), error.shape)}"
+    assert (error <= 2e-2 + 1e-2 * np.abs(expected)).all()
+
+
+LENGTHS = {
+    "one_token": [1],
+    "block_edges": [15, 16, 17, 31, 32, 33],
+    "mixed": [1, 16, 17, 47, 48, 80, 3, 64, 700, 2049],
+    "long": [5000, 4096],
+}
+
+
+@pytest.mark.parametrize("name", LENGTHS)
+@pytest.mark.parametrize("groups", [1, 2, 4, 8])
+def test_decode_qwen_shape_matches_the_oracle(hip_decode, name, groups):
+    lengths = LENGTHS[name]
+    q, pool, table, lens = decode_case(lengths, layers=3, kv_heads=2, slots=16, head_dim=128, groups=groups, seed=groups)
+    expected = oracle.decode_attention(q, pool, 1, table, lens, groups)
+    out = hip_decode.paged_decode_attention_hip(to_gpu_bf16(q), to_gpu_bf16(pool), 1, torch.from_numpy(table).cuda(),
+                                                torch.from_numpy(lens).cuda(), groups)
+    assert out.dtype == torch.bfloat16 and out.shape == q.shape
+    assert_close_to_oracle(out, expected, f"{name} G={groups}")
+
+
+@pytest.mark.parametrize("head_dim,slots,groups", [(24, 16, 2), (32, 7, 4), (128, 16, 3), (64, 4, 1), (256, 16, 2)])
+def test_decode_other_shapes_match_the_oracle(hip_decode, head_dim, slots, groups):
+    q, pool, table, lens = decode_case([1, 20, 47, 130], layers=2, kv_heads=3, slots=slots, head_dim=head_dim, groups=groups, seed=5)
+    expected = oracle.decode_attention(q, pool, 0, table, lens, groups)
+    out = hip_decode.paged_decode_attention_hip(to_gpu_bf16(q), to_gpu_bf16(pool), 0, torch.from_numpy(table).cuda(),
+                                                torch.from_numpy(lens).cuda(), groups)
+    assert_close_to_oracle(out, expected, f"D={head_dim} S={slots} G={groups}")
+
+
+def test_decode_fp32_q_and_pool(hip_decode):
+    q, pool, table, lens = decode_case([20, 333], layers=2, kv_heads=2, slots=16, head_dim=128, groups=4, seed=6)
+    expected = oracle.decode_attention(q, pool, 1, table, lens, 4)
+    qf = to_gpu_bf16(q).float()
+    for pool_tensor in (to_gpu_bf16(pool), to_gpu_bf16(pool).float()):
+        out = hip_decode.paged_decode_attention_hip(qf, pool_tensor, 1, torch.from_numpy(table).cuda(), torch.from_numpy(lens).cuda(), 4)
+        assert out.dtype == torch.float32
+        error = np.abs(out.double().cpu().numpy() - expected)
+        assert error.max() < 1e-4, (pool_tensor.dtype, error.max())
+
+
+def test_decode_unwritten_slots_cannot_poison_the_result(hip_decode):
+    q, pool, table, lens = decode_case([20, 3, 37], layers=2, kv_heads=2, slots=16, head_dim=128, groups=4, seed=7)
+    args = lambda p: (to_gpu_bf16(q), to_gpu_bf16(p), 1, torch.from_numpy(table).cuda(), torch.from_numpy(lens).cuda(), 4)
+    clean = hip_decode.paged_decode_attention_hip(*args(pool))
+    for poison in (0x7FC0, 0x7F80, 0xFF80):
+        dirty = pool.copy()
+        dirty[table[0, 1], :, :, :, 4:] = poison
+        dirty[table[1, 0], :, :, :, 3:] = poison
+        dirty[table[2, 2], :, :, :, 5:] = poison
+        out = hip_decode.paged_decode_attention_hip(*args(dirty))
+        assert torch.isfinite(out.float()).all()
+        assert torch.equal(out, clean)
+
+
+def test_decode_large_scores_and_a_moving_maximum(hip_decode):
+    q, pool, table, lens = decode_case([300, 64], layers=2, kv_heads=2, slots=16, head_dim=128, groups=4, seed=8, gain=6.0)
+    values = oracle.bf16_to_float(pool)
+    values[:, 0] *= 6
+    values[table[0, -1], 0] *= 3  # a late block with the largest scores
+    pool = oracle.bf16_bits(values)
+    expected = oracle.decode_attention(q, pool, 1, table, lens, 4)
+    out = hip_decode.paged_decode_attention_hip(to_gpu_bf16(q), to_gpu_bf16(pool), 1, torch.from_numpy(table).cuda(),
+                                                torch.from_numpy(lens).cuda(), 4)
+    assert_close_to_oracle(out, expected, "large scores")
+
+
+@pytest.mark.parametrize("layers", [4, 3], ids=["aligned_records", "unaligned_records"])
+def test_decode_fp8_pool_matches_the_oracle_on_the_dequantized_pool(fp8, hip_decode, layers):
+    kv_heads, slots, head_dim = 2, 16, 128
+    q, pool, table, lens = decode_case([1, 17, 500, 1200], layers, kv_heads, slots, head_dim, groups=4, seed=9)
+    blocks = pool.shape[0]
+    layout = fp8.Fp8Layout(slots * head_dim, 2 * layers * kv_heads)
+    records = oracle.quantize_records(pool, np.arange(blocks), layout.group_elems, layout.groups_per_block)
+    dequantized = np.zeros_like(pool)
+    oracle.dequantize_records(records, np.arange(blocks), dequantized, layout.group_elems, layout.groups_per_block)
+    expected = oracle.decode_attention(q, dequantized, 2, table, lens, 4)
+    fp8_pool = hip_decode.Fp8KVPool(torch.from_numpy(records.reshape(blocks, -1)).cuda(), layers, kv_heads, slots, head_dim)
+    out = hip_decode.paged_decode_attention_hip(to_gpu_bf16(q), fp8_pool, 2, torch.from_numpy(table).cuda(), torch.from_numpy(lens).cuda(), 4)
+    assert_close_to_oracle(out, expected, "fp8 records")
+
+
+@pytest.mark.parametrize("layers", [4, 1], ids=["fast_kernel", "generic_kernel"])
+def test_decode_fp8_pool_with_extreme_shifts_uses_the_exact_decode(fp8, hip_decode, layers):
+    kv_heads, slots, head_dim = 2, 16, 128
+    q, pool, table, lens = decode_case([40], layers, kv_heads, slots, head_dim, groups=2, seed=10)
+    values = oracle.bf16_to_float(pool)
+    values[:, 0] *= 2.0**-120  # K groups with shifts near -127
+    values[:, 1] *= 2.0**-115  # V groups with shifts near -120
+    pool = oracle.bf16_bits(values)
+    layout = fp8.Fp8Layout(slots * head_dim, 2 * layers * kv_heads)
+    blocks = pool.shape[0]
+    records = oracle.quantize_records(pool, np.arange(blocks), layout.group_elems, layout.groups_per_block)
+    dequantized = np.zeros_like(pool)
+    oracle.dequantize_records(records, np.arange(blocks), dequantized, layout.group_elems, layout.groups_per_block)
+    q = oracle.bf16_bits(oracle.bf16_to_float(q) * 2.0**118)
+    expected = oracle.decode_attention(q, dequantized, layers - 1, table, lens, 2)
+    fp8_pool = hip_decode.Fp8KVPool(torch.from_numpy(records.reshape(blocks, -1)).cuda(), layers, kv_heads, slots, head_dim)
+    out = hip_decode.paged_decode_attention_hip(to_gpu_bf16(q), fp8_pool, layers - 1, torch.from_numpy(table).cuda(), torch.from_numpy(lens).cuda(), 2)
+    got = out.double().cpu().numpy()
+    assert np.isfinite(got).all()
+    assert (np.abs(got - expected) <= np.abs(expected) * 2.0**-7 + 2.0**-126).all()
+
+
+@pytest.mark.parametrize(
+    "mutate",
+    [
+        lambda c: {**c, "lengths": torch.tensor([0, 5], dtype=torch.int32, device="cuda")},
+        lambda c: {**c, "lengths": torch.tensor([33, 5], dtype=torch.int32, device="cuda")},
+        lambda c: {**c, "table": torch.tensor([[0, 99], [1, 2]], dtype=torch.int32, device="cuda")},
+        lambda c: {**c, "table": torch.tensor([[0, -1], [1, 2]], dtype=torch.int32, device="cuda")},
+        lambda c: {**c, "layer": 3},
+        lambda c: {**c, "groups": 3},
+        lambda c: {**c, "q": c["q"][:, :, :-1]},
+        lambda c: {**c, "q": c["q"][:1]},
+        lambda c: {**c, "pool": c["pool"].transpose(0, 1)},
+        lambda c: {**c, "pool": c["pool"][::2]},
+        lambda c: {**c, "q": c["q"].double()},
+        lambda c: {**c, "pool": c["pool"].double()},
+    ],
+    ids=["empty_sequence", "longer_than_table", "block_past_pool", "negative_block", "layer_past_pool", "groups_disagree",
+         "head_dim_disagrees", "batch_disagrees", "kinds_not_two", "non_contiguous_pool", "q_float64", "pool_float64"],
+)
+def test_decode_invalid_inputs_are_refused_before_launch(hip_decode, mutate):
+    q, pool, table, lens = decode_case([20, 5], layers=3, kv_heads=2, slots=16, head_dim=24, groups=2, seed=41)
+    good = dict(q=to_gpu_bf16(q), pool=to_gpu_bf16(pool), table=torch.from_numpy(table).cuda(), lengths=torch.from_numpy(lens).cuda(), layer=1, groups=2)
+    bad = mutate(good)
+    with pytest.raises(ValueError):
+        hip_decode.paged_decode_attention_hip(bad["q"], bad["pool"], bad["layer"], bad["table"], bad["lengths"], bad["groups"])
+
+
+def test_decode_int64_table_and_non_contiguous_q(hip_decode):
+    q, pool, table, lens = decode_case([20, 40], layers=2, kv_heads=2, slots=16, head_dim=128, groups=2, seed=35)
+    args = (to_gpu_bf16(pool), 1)
+    expected = hip_decode.paged_decode_attention_hip(to_gpu_bf16(q), *args, torch.from_numpy(table).cuda(), torch.from_numpy(lens).cuda(), 2)
+    strided = torch.zeros(2, 8, 128, dtype=torch.bfloat16, device="cuda")
+    strided[:, ::2] = to_gpu_bf16(q)
+    got = hip_decode.paged_decode_attention_hip(strided[:, ::2], *args, torch.from_numpy(table).long().cuda(), torch.from_numpy(lens).long().cuda(), 2)
+    assert torch.equal(got, expected)
+
+
+def test_decode_block_offsets_past_32_bits(hip_decode):
+    layers, kv_heads, slots, head_dim = 36, 2, 16, 128
+    stride = 2 * layers * kv_heads * slots * head_dim
+    blocks = 2**31 // stride + 8
+    pool = torch.zeros(blocks, 2, layers, kv_heads, slots, head_dim, dtype=torch.bfloat16, device="cuda")
+    q, small, _, lens = decode_case([40], layers, kv_heads, slots, head_dim, groups=1, seed=40, pool_blocks=3)
+    ids = [blocks - 1, blocks - 5, 3]
+    pool[torch.tensor(ids, device="cuda")] = to_gpu_bf16(small)
+    out = hip_decode.paged_decode_attention_hip(to_gpu_bf16(q), pool, 7, torch.tensor([ids], dtype=torch.int32, device="cuda"),
+                                                torch.from_numpy(lens).cuda(), 1)
+    expected = oracle.decode_attention(q, small, 7, np.arange(3, dtype=np.int32)[None], lens, 1)
+    assert_close_to_oracle(out, expected, "64-bit offsets")
+    del pool
+    torch.cuda.empty_cache()
