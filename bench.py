@@ -1,0 +1,411 @@
+"""Benchmark of the KV data path on one MI355X.
+
+Headline: FP8 swap-out + swap-in of 8,192 tokens (512 random
+Qwen3-4B blocks of a 12 GiB BF16 pool with 0.1% +/-40 outliers) through NativeBackend: fused
+gather+quantize into staging, SDMA to pinned host memory, then SDMA back and fused
+dequantize+scatter into 512 fresh random block ids. A step is one out+in; `value` is ms per
+step (lower is better). Inputs are resident in HBM when the timed region starts.
+
+Also measured in the same run (extra keys of the JSON line):
+  link        pinned hipMemcpyAsync peak each way (the host-link roofline of the swap)
+  roofline    the fused quantize kernel: algorithmic bytes / its average duration, from HIP
+              events recorded on the stream it runs on, against the 8 TB/s HBM peak
+  decode      BASELINE configs[2]: paged decode, batch 32, contexts U[1024, 32768], 36
+              layers timed per layer, "unique" KV bytes (decode_bandwidth.py:129-139)
+  decode_fp8  configs[3]: the same reading FP8 records, plus batch 1 @ 32,768 and 64 @ 4,096
+  cpu_baseline  the oracle's C restatement of the FP8 swap arithmetic on a bounded sample,
+              single-threaded on the host cores
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-decode] [--skip-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+L4_FP8_SWAP_MS = 67.0  # README.md:27, :115 of the reference (NVIDIA L4)
+QWEN = dict(layers=36, kv_heads=8, query_heads=32, slots=16, head_dim=128)
+POOL_BYTES = 12 << 30
+
+
+def log(message: str) -> None:
+    print(f"[bench] {message}", file=sys.stderr, flush=True)
+
+
+def fill_pool(pool, seed: int, outlier_fraction: float = 0.0) -> None:
+    """N(0,1) BF16 plus seeded +/-40 outliers, filled in slices to bound temporaries."""
+    import torch
+
+    generator = torch.Generator(device=pool.device).manual_seed(seed)
+    for start in range(0, pool.shape[0], 256):
+        piece = pool[start : start + 256]
+        values = torch.randn(piece.shape, generator=generator, device=pool.device, dtype=torch.float32)
+        if outlier_fraction:
+            mask = torch.rand(piece.shape, generator=generator, device=pool.device) < outlier_fraction
+            signs = torch.where(torch.rand(piece.shape, generator=generator, device=pool.device) < 0.5, -40.0, 40.0)
+            values = torch.where(mask, signs, values)
+        piece.copy_(values.to(torch.bfloat16))
+        del values
+
+
+class KernelTimer:
+    """Wraps an FP8 kernel so each launch is bracketed by HIP events on the stream it is
+    launched on (the backend's own stream), for the kernel's average duration."""
+
+    def __init__(self, kernel, bytes_of):
+        self.kernel = kernel
+        self.bytes_of = bytes_of
+        self.events = []
+        self.recording = False
+
+    def __call__(self, *args):
+        import torch
+
+        if not self.recording:
+            return self.kernel(*args)
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        self.kernel(*args)
+        end.record()
+        self.events.append((start, end, self.bytes_of(*args)))
+
+    def summary(self):
+        times = [s.elapsed_time(e) for s, e, _ in self.events]
+        total_bytes = sum(b for _, _, b in self.events)
+        launches = len(times)
+        mean_ms = sum(times) / launches
+        return {"launches": launches, "mean_ms": mean_ms, "bytes_per_launch": total_bytes / launches,
+                "achieved_gbs": total_bytes / (sum(times) * 1e-3) / 1e9}
+
+
+def measure_link(device, nbytes: int = 512 << 20, repeats: int = 5) -> dict:
+    """Pinned-memory hipMemcpyAsync peak each way (torch copies are SDMA copies here)."""
+    import torch
+
+    host = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+    dev = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    out = {}
+    stream = torch.cuda.Stream(device=device)
+    for name, fn in (("d2h_gbs", lambda: host.copy_(dev, non_blocking=True)), ("h2d_gbs", lambda: dev.copy_(host, non_blocking=True))):
+        with torch.cuda.stream(stream):
+            fn()
+            stream.synchronize()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            for _ in range(repeats):
+                fn()
+            end.record()
+            end.synchronize()
+        out[name] = repeats * nbytes / (start.elapsed_time(end) * 1e-3) / 1e9
+    out["bytes"] = nbytes
+    return out
+
+
+def swap_bench(args, device, pool_blocks: int, cache):
+    import numpy as np
+    import torch
+
+    from layover_amd.kernels.fp8 import Fp8Layout, dequantize_blocks, quantize_blocks
+    from layover_amd.kv.transfer import NativeBackend
+    from oracle import oracle
+
+    layout = Fp8Layout.from_cache(cache)
+    rng = np.random.default_rng(1)
+    chosen = rng.permutation(pool_blocks)[: 2 * args.blocks]
+    src = [int(i) for i in chosen[: args.blocks]]
+    dst = [int(i) for i in chosen[args.blocks :]]
+
+    quantize_timer = KernelTimer(quantize_blocks, lambda pool, ids, stage, lay: ids.shape[0] * (2 * lay.block_elems + lay.record_bytes))
+    dequantize_timer = KernelTimer(lambda stage, ids, pool, lay: dequantize_blocks(stage, ids, pool, lay),
+                                   lambda stage, ids, pool, lay: ids.shape[0] * (2 * lay.block_elems + lay.record_bytes))
+    backend = NativeBackend(device, staging_bytes=args.staging_mib << 20, num_staging=2, ids_capacity=1 << 20,
+                            fp8_kernels=(quantize_timer, dequantize_timer))
+    backend.prepare(cache, fp8=True)
+
+    def step():
+        out = backend.start_out(cache, src, fp8=True)
+        out.wait()
+        backend.start_in(cache, dst, out.payload).wait()
+        return out.payload
+
+    log(f"swap: warmup {args.warmup}")
+    for _ in range(args.warmup):
+        backend.free(step())
+
+    # Parity on a sample of records: payload bytes vs the oracle's records, restored blocks
+    # vs the oracle's dequantization of them.
+    payload = step()
+    sample = list(range(0, args.blocks, max(1, args.blocks // 4)))[:4]
+    bits = cache.pool[torch.tensor([src[i] for i in sample], device=device)].view(torch.int16).cpu().numpy().view(np.uint16)
+    expected = oracle.quantize_records(bits, list(range(len(sample))), layout.group_elems, layout.groups_per_block)
+    memory = payload.memory.numpy()
+    got = np.concatenate([memory[i * layout.record_bytes : (i + 1) * layout.record_bytes] for i in sample])
+    restored = cache.pool[torch.tensor([dst[i] for i in sample], device=device)].view(torch.int16).cpu().numpy().view(np.uint16)
+    reference = np.zeros_like(bits)
+    oracle.dequantize_records(expected, list(range(len(sample))), reference, layout.group_elems, layout.groups_per_block)
+    parity = bool(np.array_equal(got, expected) and np.array_equal(restored, reference))
+    backend.free(payload)
+    if not parity:
+        raise SystemExit("FP8 swap is not bit-exact against the oracle: refusing to report a number")
+
+    log(f"swap: timing {args.steps} steps")
+    quantize_timer.recording = dequantize_timer.recording = True
+    torch.cuda.synchronize()
+    start = time.perf_counter()
+    out_ms, in_ms = [], []
+    for _ in range(args.steps):
+        t0 = time.perf_counter()
+        out = backend.start_out(cache, src, fp8=True)
+        out.wait()
+        t1 = time.perf_counter()
+        backend.start_in(cache, dst, out.payload).wait()
+        t2 = time.perf_counter()
+        backend.free(out.payload)
+        out_ms.append((t1 - t0) * 1e3)
+        in_ms.append((t2 - t1) * 1e3)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - start
+    quantize_timer.recording = dequantize_timer.recording = False
+    stats = backend.engine.stats()
+    backend.close()
+    record_total = args.blocks * layout.record_bytes
+    return {
+        "ms_per_step": elapsed * 1e3 / args.steps,
+        "out_ms": sorted(out_ms)[len(out_ms) // 2],
+        "in_ms": sorted(in_ms)[len(in_ms) // 2],
+        "bytes_each_way": record_total,
+        "bf16_bytes_each_way": args.blocks * cache.block_bytes,
+        "quantize": quantize_timer.summary(),
+        "dequantize": dequantize_timer.summary(),
+        "parity_sample_records": len(sample),
+        "segments_per_direction": math.ceil(args.blocks / ((args.staging_mib << 20) // layout.record_bytes)),
+        "engine_memcpys": stats["memcpys"],
+    }
+
+
+def decode_tables(rng, batch: int, lengths, pool_blocks: int, distinct: bool):
+    import numpy as np
+
+    width = max(-(-int(n) // 16) for n in lengths)
+    table = np.zeros((batch, width), dtype=np.int32)
+    if distinct:
+        ids = rng.permutation(pool_blocks)
+        at = 0
+        for b, n in enumerate(lengths):
+            k = -(-int(n) // 16)
+            table[b, :k] = ids[at : at + k]
+            at += k
+    else:
+        for b, n in enumerate(lengths):
+            k = -(-int(n) // 16)
+            table[b, :k] = rng.choice(pool_blocks, k, replace=False)
+    return table
+
+
+def decode_bench(device, pool, lengths, steps: int, warmup: int, seed: int, distinct: bool = False, kv_pool=None):
+    """Time 36 single-layer launches per step; bytes are the reference's unique accounting."""
+    import numpy as np
+    import torch
+
+    from layover_amd.kernels import hip_decode
+
+    rng = np.random.default_rng(seed)
+    batch = len(lengths)
+    pool_blocks = pool.shape[0]
+    table = torch.from_numpy(decode_tables(rng, batch, lengths, pool_blocks, distinct)).to(device)
+    lens = torch.tensor(lengths, dtype=torch.int32, device=device)
+    generator = torch.Generator(device=device).manual_seed(seed)
+    q = torch.randn(batch, QWEN["query_heads"], QWEN["head_dim"], generator=generator, device=device).to(torch.bfloat16)
+    target = kv_pool if kv_pool is not None else pool
+    out = torch.empty_like(q)
+    shape = hip_decode.decode_shape(q, target, 0, table, QWEN["query_heads"] // QWEN["kv_heads"])
+    workspace = torch.empty(hip_decode.workspace_bytes(shape), dtype=torch.uint8, device=device)
+    groups = QWEN["query_heads"] // QWEN["kv_heads"]
+    for _ in range(warmup):
+        for layer in range(QWEN["layers"]):
+            hip_decode.run_kernel(q, target, layer, table, lens, groups, out, workspace)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        for layer in range(QWEN["layers"]):
+            hip_decode.run_kernel(q, target, layer, table, lens, groups, out, workspace)
+    end.record()
+    end.synchronize()
+    per_layer_ms = start.elapsed_time(end) / (steps * QWEN["layers"])
+    blocks = sum(-(-int(n) // 16) for n in lengths)
+    tile = QWEN["slots"] * QWEN["head_dim"]
+    if kv_pool is not None:
+        kv_bytes = blocks * QWEN["kv_heads"] * 2 * (tile + 2)
+    else:
+        kv_bytes = blocks * QWEN["kv_heads"] * 2 * tile * 2
+    other = q.numel() * 2 * 2 + table.numel() * 4 + batch * 4
+    return {
+        "batch": batch,
+        "per_layer_us": per_layer_ms * 1e3,
+        "kv_bytes_per_layer": kv_bytes,
+        "achieved_gbs": (kv_bytes + other) / (per_layer_ms * 1e-3) / 1e9,
+        "frac_of_hbm_peak": (kv_bytes + other) / (per_layer_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "distinct_blocks": distinct,
+    }
+
+
+def cpu_baseline(layout, blocks_sample: int) -> dict:
+    """The oracle's single-threaded C FP8 quantize + dequantize over a sample of blocks, scaled
+    to the 512-block workload."""
+    import numpy as np
+
+    from oracle import oracle
+
+    rng = np.random.default_rng(0)
+    bits = oracle.bf16_bits(rng.standard_normal((blocks_sample, layout.block_elems), dtype=np.float32))
+    ids = np.arange(blocks_sample, dtype=np.int32)
+    start = time.perf_counter()
+    records = oracle.quantize_records(bits, ids, layout.group_elems, layout.groups_per_block)
+    restored = np.zeros_like(bits)
+    oracle.dequantize_records(records, ids, restored, layout.group_elems, layout.groups_per_block)
+    seconds = time.perf_counter() - start
+    return {"seconds": seconds, "blocks": blocks_sample}
+
+
+def main() -> None:
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--blocks", type=int, default=512, help="blocks per swap (512 = 8,192 tokens)")
+    parser.add_argument("--staging-mib", type=int, default=128)
+    parser.add_argument("--decode-steps", type=int, default=5)
+    parser.add_argument("--skip-decode", action="store_true")
+    parser.add_argument("--skip-cpu", action="store_true")
+    parser.add_argument("--cpu-blocks", type=int, default=64)
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this KV data path has no multi-GPU step (--gpus {args.gpus} refused)", file=sys.stderr)
+        raise SystemExit(2)
+
+    import numpy as np
+    import torch
+
+    from layover_amd.config import ModelConfig
+    from layover_amd.kernels.fp8 import Fp8Layout, quantize_blocks
+    from layover_amd.kernels.hip_decode import Fp8KVPool
+    from layover_amd.kv.paged_cache import PagedKVCache
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    config = ModelConfig.qwen3_4b()
+    block_bytes = 2 * config.num_hidden_layers * config.num_key_value_heads * 16 * config.head_dim * 2
+    pool_blocks = POOL_BYTES // block_bytes
+    log(f"pool: {pool_blocks} blocks of {block_bytes} B (12 GiB), filling")
+    cache = PagedKVCache(config, pool_blocks, device=device, fill=False)
+    fill_pool(cache.pool, seed=0, outlier_fraction=0.001)
+    torch.cuda.synchronize()
+
+    log("link probe")
+    link = measure_link(device)
+    swap = swap_bench(args, device, pool_blocks, cache)
+    layout = Fp8Layout.from_cache(cache)
+    bytes_round_trip = 2 * swap["bytes_each_way"]
+    link_peak = 1.0 / (1.0 / link["d2h_gbs"] + 1.0 / link["h2d_gbs"]) * 2  # harmonic: one out then one in
+    swap_gbs = bytes_round_trip / (swap["ms_per_step"] * 1e-3) / 1e9
+    q = swap["quantize"]
+
+    result = {
+        "metric": "FP8 KV swap out+in ms @8192 tok; paged decode attn achieved HBM GB/s",
+        "value": round(swap["ms_per_step"], 3),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(swap["ms_per_step"], 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": round(swap["ms_per_step"] / L4_FP8_SWAP_MS, 4),
+        "dtype": "bf16->fp8e4m3 (integer codec)",
+        "data": "synthetic: N(0,1) BF16 KV + 0.1% +/-40 outliers, seed 0; random-init Qwen3-4B KV shape",
+        "config": {
+            "workload": "fp8_swap_out_in_8192_tokens",
+            "model_kv_shape": "Qwen3-4B (36 layers x K,V x 8 kv heads x 16 slots x 128 dims, bf16)",
+            "pool_gib": 12,
+            "pool_blocks": pool_blocks,
+            "blocks": args.blocks,
+            "tokens": args.blocks * 16,
+            "staging_mib": args.staging_mib,
+            "num_staging": 2,
+        },
+        "swap": {
+            "out_ms": round(swap["out_ms"], 3),
+            "in_ms": round(swap["in_ms"], 3),
+            "bytes_each_way": swap["bytes_each_way"],
+            "round_trip_gbs": round(swap_gbs, 2),
+            "frac_of_link_peak": round(swap_gbs / link_peak, 4),
+            "parity": f"bit-exact vs oracle on {swap['parity_sample_records']} sampled records and their restored blocks",
+            "segments_per_direction": swap["segments_per_direction"],
+        },
+        "link": {"d2h_gbs": round(link["d2h_gbs"], 2), "h2d_gbs": round(link["h2d_gbs"], 2), "probe_bytes": link["bytes"],
+                 "kind": "pinned hipMemcpyAsync, measured in this run"},
+        "roofline": {
+            "kernel": "quantize_groups_2048 (fused gather + FP8 quantize)",
+            "bound": "hbm",
+            "achieved": round(q["achieved_gbs"], 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(q["achieved_gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": q["bytes_per_launch"],
+            "mean_launch_us": round(q["mean_ms"] * 1e3, 2),
+            "launches": q["launches"],
+        },
+        "dequantize_kernel": {"achieved_gbs": round(swap["dequantize"]["achieved_gbs"], 1),
+                              "mean_launch_us": round(swap["dequantize"]["mean_ms"] * 1e3, 2),
+                              "frac": round(swap["dequantize"]["achieved_gbs"] / HBM_PEAK_GBS, 4)},
+    }
+
+    if not args.skip_decode:
+        rng = np.random.default_rng(2)
+        mixed = [int(n) for n in rng.integers(1024, 32769, size=32)]
+        log("decode bf16 (config 3)")
+        decode = decode_bench(device, cache.pool, mixed, args.decode_steps, 1, seed=3)
+        result["decode"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in decode.items()}
+        result["decode"]["lengths"] = "U[1024, 32768], batch 32, seed 2; rows sampled from the 12 GiB pool (blocks alias across rows)"
+        log("decode fp8 records (config 4)")
+        records = torch.empty(pool_blocks, layout.record_bytes, dtype=torch.uint8, device=device)
+        for first in range(0, pool_blocks, 512):
+            ids = torch.arange(first, min(pool_blocks, first + 512), dtype=torch.int32, device=device)
+            quantize_blocks(cache.pool, ids, records[first:].reshape(-1), layout)
+        fp8_pool = Fp8KVPool(records, config.num_hidden_layers, config.num_key_value_heads, 16, config.head_dim)
+        fp8_runs = []
+        for name, lengths in (("batch32_mixed", mixed), ("batch1_32768", [32768]), ("batch64_4096", [4096] * 64)):
+            run = decode_bench(device, cache.pool, lengths, args.decode_steps, 1, seed=4, kv_pool=fp8_pool)
+            fp8_runs.append({"case": name, **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in run.items()}})
+        result["decode_fp8"] = fp8_runs
+        del records, fp8_pool
+        torch.cuda.empty_cache()
+
+    if not args.skip_cpu:
+        log(f"cpu baseline: oracle FP8 quantize+dequantize on {args.cpu_blocks} blocks")
+        cpu = cpu_baseline(layout, args.cpu_blocks)
+        scaled_ms = cpu["seconds"] * 1e3 * args.blocks / cpu["blocks"]
+        result["cpu_baseline"] = {
+            "value": round(scaled_ms, 1),
+            "unit": "ms",
+            "cores": 1,
+            "kind": "port",
+            "sample": f"oracle C quantize+dequantize of {cpu['blocks']} Qwen3-4B blocks ({cpu['seconds']:.2f} s), scaled to {args.blocks} blocks; arithmetic only, no host copies",
+        }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()
