@@ -278,6 +278,19 @@ def cpu_baseline(layout, blocks_sample: int) -> dict:
     return {"seconds": seconds, "blocks": blocks_sample}
 
 
+def calibrate_copy(device, nbytes: int = 1 << 30) -> None:
+    """One plain elementwise copy of known size (read nbytes, write nbytes), so hardware
+    byte counters (FETCH_SIZE, WRITE_SIZE) of the kernels above can be scaled by what the
+    same counters read for a kernel whose traffic is known."""
+    import torch
+
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device=device)
+    dst = torch.empty_like(src)
+    torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def main() -> None:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
@@ -404,6 +417,7 @@ def main() -> None:
             "kind": "port",
             "sample": f"oracle C quantize+dequantize of {cpu['blocks']} Qwen3-4B blocks ({cpu['seconds']:.2f} s), scaled to {args.blocks} blocks; arithmetic only, no host copies",
         }
+    calibrate_copy(device)
     print(json.dumps(result), flush=True)
 
 

@@ -1,0 +1,66 @@
+"""The C-ABI libraries load without a GPU and export exactly what include/*.h declares.
+No compute calls: on a machine without a GPU only loading and symbol lookup are checked."""
+
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from layover_amd.kernels import _lib
+from layover_amd.kv import native
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared(header: str) -> set[str]:
+    text = (ROOT / "include" / header).read_text()
+    return set(re.findall(r"^\s*(?:int|uint64_t|const char\*)\s+(l[tk]_\w+)\(", text, flags=re.M))
+
+
+def exported(path: Path) -> set[str]:
+    out = subprocess.run(["nm", "-D", "--defined-only", str(path)], check=True, capture_output=True, text=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if " T " in line}
+
+
+def test_transfer_header_declares_the_reference_abi():
+    names = declared("layover_transfer.h")
+    assert len(names) == 26
+    assert {"lt_out_gather", "lt_in_scatter", "lt_ext_copy_out", "lt_ext_finish", "lt_host_set_pin_limit"} <= names
+    assert set(native.SIGNATURES) | {"lt_abi_version", "lt_flavor", "lt_last_error"} == names
+
+
+@pytest.mark.parametrize("flavor", ["host", "hip"])
+def test_transfer_library_exports_every_declared_symbol(flavor):
+    path = native.library_path(flavor)
+    assert path.exists(), f"{path} is not built"
+    symbols = exported(path)
+    assert declared("layover_transfer.h") <= symbols
+    assert not {s for s in symbols if s.startswith(("hip", "__hip"))}, "the library must not re-export the HIP runtime"
+
+
+def test_kernel_library_exports_every_declared_symbol():
+    path = _lib.library_path()
+    assert path.exists(), f"{path} is not built"
+    names = declared("layover_kernels.h")
+    assert names == {"lk_abi_version", "lk_last_error", "lk_fp8_quantize", "lk_fp8_dequantize", "lk_fp8_encode",
+                     "lk_fp8_decode", "lk_paged_decode_workspace", "lk_paged_decode"}
+    assert names <= exported(path)
+    assert set(_lib.SIGNATURES) | {"lk_abi_version", "lk_last_error"} == names
+
+
+def test_hip_libraries_load_into_one_hip_runtime_without_a_gpu():
+    lib = native.load_library("hip")
+    assert lib.lt_abi_version() == 2 and lib.lt_flavor() == b"hip"
+    kernels = _lib.load()
+    assert kernels.lk_abi_version() == 1
+    assert len(native.hip_runtimes_loaded()) == 1
+
+
+def test_decode_workspace_depends_on_shape_only_and_refuses_nonsense():
+    kernels = _lib.load()
+    shape = _lib.DecodeShape(32, 32, 8, 128, 36, 16, 0, 2048, _lib.LK_BF16, _lib.LK_BF16, 128**-0.5)
+    size = kernels.lk_paged_decode_workspace(shape)
+    assert size > 0 and size % 4 == 0
+    bad = _lib.DecodeShape(32, 30, 8, 128, 36, 16, 0, 2048, _lib.LK_BF16, _lib.LK_BF16, 1.0)
+    assert kernels.lk_paged_decode_workspace(bad) == 0
