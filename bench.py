@@ -345,7 +345,7 @@ def main() -> None:
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": round(swap["ms_per_step"] / L4_FP8_SWAP_MS, 4),
-        "dtype": "bf16->fp8e4m3 (integer codec)",
+        "dtype": "bf16->fp8e4m3 (RNE codec, bit-exact)",
         "data": "synthetic: N(0,1) BF16 KV + 0.1% +/-40 outliers, seed 0; random-init Qwen3-4B KV shape",
         "config": {
             "workload": "fp8_swap_out_in_8192_tokens",

@@ -84,84 +84,17 @@ __device__ __forceinline__ uint32_t wave_max(uint32_t value) {
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-// Qwen3-shaped groups: 2048 values, everything 16-byte aligned.
+// Qwen3-shaped groups (2048 values, 16-byte aligned records) run the kernels of
+// fp8_records.hip; these launch them on `stream`.
 constexpr uint32_t kFastGroup = 2048;
+void launch_quantize_2048(const uint16_t* pool, const int32_t* ids, uint8_t* stage, uint32_t count, uint32_t groups_per_block,
+                          uint32_t grid, hipStream_t stream);
+void launch_dequantize_2048(const uint8_t* stage, const int32_t* ids, uint16_t* pool, uint32_t count, uint32_t groups_per_block,
+                            uint32_t grid, hipStream_t stream);
 
-__global__ __launch_bounds__(kWave* kCodecWaves) void quantize_groups_2048(const uint16_t* __restrict__ pool,
-                                                                         const int32_t* __restrict__ ids, uint8_t* __restrict__ stage,
-                                                                         uint32_t count, uint32_t groups_per_block) {
-    const uint32_t lane = threadIdx.x % kWave;
-    const uint64_t group = uint64_t(blockIdx.x) * kCodecWaves + threadIdx.x / kWave;
-    if (group >= uint64_t(count) * groups_per_block) return;
-    const uint32_t index = uint32_t(group / groups_per_block);
-    const uint32_t g = uint32_t(group % groups_per_block);
-    const uint64_t block_elems = uint64_t(kFastGroup) * groups_per_block;
-    const uint64_t record = block_elems + 2ull * groups_per_block;
-    const u32x4* source = reinterpret_cast<const u32x4*>(pool + uint64_t(ids[index]) * block_elems + uint64_t(g) * kFastGroup);
-
-    u32x4 words[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) words[j] = __builtin_nontemporal_load(source + j * kWave + lane);
-
-    uint32_t key = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const uint32_t lo = exponent_key(words[j][w] & 0xFFFFu), hi = exponent_key(words[j][w] >> 16);
-            key = lo > key ? lo : key;
-            key = hi > key ? hi : key;
-        }
-    const int32_t shift = shift_from_key(wave_max(key));
-
-    uint8_t* out = stage + uint64_t(index) * record;
-    u32x2* codes = reinterpret_cast<u32x2*>(out + uint64_t(g) * kFastGroup);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        uint32_t packed[2];
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            const uint32_t a = words[j][2 * half], b = words[j][2 * half + 1];
-            packed[half] = encode_e4m3(a & 0xFFFFu, shift) | (encode_e4m3(a >> 16, shift) << 8) |
-                           (encode_e4m3(b & 0xFFFFu, shift) << 16) | (encode_e4m3(b >> 16, shift) << 24);
-        }
-        codes[j * kWave + lane] = u32x2{packed[0], packed[1]};
-    }
-    if (lane == 0) {
-        const int16_t stored = int16_t(shift);
-        *reinterpret_cast<int16_t*>(out + block_elems + 2ull * g) = stored;
-    }
-}
-
-__global__ __launch_bounds__(kWave* kCodecWaves) void dequantize_groups_2048(const uint8_t* __restrict__ stage,
-                                                                           const int32_t* __restrict__ ids, uint16_t* __restrict__ pool,
-                                                                           uint32_t count, uint32_t groups_per_block) {
-    const uint32_t lane = threadIdx.x % kWave;
-    const uint64_t group = uint64_t(blockIdx.x) * kCodecWaves + threadIdx.x / kWave;
-    if (group >= uint64_t(count) * groups_per_block) return;
-    const uint32_t index = uint32_t(group / groups_per_block);
-    const uint32_t g = uint32_t(group % groups_per_block);
-    const uint64_t block_elems = uint64_t(kFastGroup) * groups_per_block;
-    const uint64_t record = block_elems + 2ull * groups_per_block;
-    const uint8_t* in = stage + uint64_t(index) * record;
-    const int32_t shift = *reinterpret_cast<const int16_t*>(in + block_elems + 2ull * g);
-    const u32x2* codes = reinterpret_cast<const u32x2*>(in + uint64_t(g) * kFastGroup);
-    u32x4* target = reinterpret_cast<u32x4*>(pool + uint64_t(ids[index]) * block_elems + uint64_t(g) * kFastGroup);
-
-    u32x2 bytes[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) bytes[j] = __builtin_nontemporal_load(codes + j * kWave + lane);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        u32x4 out;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            const uint32_t word = bytes[j][w / 2] >> (16 * (w % 2));
-            out[w] = decode_e4m3(word & 0xFFu, shift) | (decode_e4m3((word >> 8) & 0xFFu, shift) << 16);
-        }
-        target[j * kWave + lane] = out;
-    }
-}
+// Kernels below have internal linkage: this header is included by more than one translation
+// unit of the library.
+namespace {
 
 // Any group size and alignment: element-strided loops, one wave per group.
 __global__ __launch_bounds__(kWave* kCodecWaves) void quantize_groups_any(const uint16_t* __restrict__ pool, const int32_t* __restrict__ ids,
@@ -215,6 +148,8 @@ __global__ void decode_elements(const uint8_t* __restrict__ codes, uint16_t* __r
     const uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (i < n) out[i] = uint16_t(decode_e4m3(codes[i], shift));
 }
+
+}  // namespace
 
 }  // namespace lk
 

@@ -1,0 +1,161 @@
+// Fused gather+quantize and dequantize+scatter of Qwen3-shaped FP8 records (2048-value
+// groups, 16-byte aligned records), the kernels of lk_fp8_quantize / lk_fp8_dequantize.
+//
+// This translation unit is compiled with FP32 denormals flushed to zero (Makefile), which
+// the fast path relies on. Each wave takes one group:
+//
+// quantize: one pass over the group's 32 values per lane computes, on BF16 pairs packed in
+//   32-bit words, the masked exponent plus one step (so infinity/NaN wrap to 0 and set bit
+//   15 of their half, flagging the group) and a packed 16-bit max; a wave max gives the
+//   shift (fp8.py:86-92). Then, when the group has no infinity/NaN and shift >= -126:
+//     code = cvt_fp8_e4m3_rne(float(bf16) * 2^-shift)     (v_cvt_pk_fp8_f32)
+//   float(bf16) * 2^-shift is exact (a BF16 value times a power of two), so the one
+//   rounding is the convert's round-to-nearest-even, as in fp8.py:103-109; BF16
+//   subnormals are flushed to signed zero by the multiply (denormals off), as fp8.py:114
+//   requires; and the computed shift keeps every value below 2^8, far from E4M3's 448, so
+//   nothing saturates. Other groups run the reference's integer codec (encode_e4m3).
+// dequantize: with no NaN code in the group (a SWAR byte test) and a shift in [-117, 119],
+//     bf16 = high half of float(e4m3) * 2^shift              (v_cvt_pk_f32_fp8, v_perm)
+//   is exact: every E4M3 value times such a power of two is a BF16 normal (or zero) below
+//   0x7F7F, so fp8.py:133-134's saturation and flush never apply. Otherwise decode_e4m3.
+// Both fast paths are checked bit for bit against the integer codec on every BF16 pattern
+// at every shift the computed scale can take (tests/test_gpu_kernels.py).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fp8_codec.h"
+
+namespace lk {
+
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float power_of_two(int32_t e) { return __uint_as_float(uint32_t(e + 127) << 23); }
+
+__global__ __launch_bounds__(kWave* kCodecWaves) void quantize_groups_2048(const uint16_t* __restrict__ pool,
+                                                                         const int32_t* __restrict__ ids, uint8_t* __restrict__ stage,
+                                                                         uint32_t count, uint32_t groups_per_block) {
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint64_t group = uint64_t(blockIdx.x) * kCodecWaves + threadIdx.x / kWave;
+    if (group >= uint64_t(count) * groups_per_block) return;
+    const uint32_t index = uint32_t(group / groups_per_block);
+    const uint32_t g = uint32_t(group % groups_per_block);
+    const uint64_t block_elems = uint64_t(kFastGroup) * groups_per_block;
+    const uint64_t record = block_elems + 2ull * groups_per_block;
+    const u32x4* source = reinterpret_cast<const u32x4*>(pool + uint64_t(ids[index]) * block_elems + uint64_t(g) * kFastGroup);
+
+    u32x4 words[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) words[j] = __builtin_nontemporal_load(source + j * kWave + lane);
+
+    u16x2 keys = {0, 0};
+    uint32_t flags = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const uint32_t stepped = (words[j][w] & 0x7F807F80u) + 0x00800080u;
+            flags |= stepped;
+            keys = __builtin_elementwise_max(keys, __builtin_bit_cast(u16x2, stepped & 0x7FFF7FFFu));
+        }
+    const uint32_t lane_key = uint32_t(keys.x > keys.y ? keys.x : keys.y) >> 7;
+    const int32_t shift = shift_from_key(wave_max(lane_key));
+    const bool nonfinite = __any((flags & 0x80008000u) != 0);
+
+    uint8_t* out = stage + uint64_t(index) * record;
+    u32x2* codes = reinterpret_cast<u32x2*>(out + uint64_t(g) * kFastGroup);
+    if (!nonfinite && shift >= -126) {
+        const float scale = power_of_two(-shift);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint32_t packed[2];
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                const uint32_t a = words[j][2 * half], b = words[j][2 * half + 1];
+                int p = __builtin_amdgcn_cvt_pk_fp8_f32(__uint_as_float(a << 16) * scale, __uint_as_float(a & 0xFFFF0000u) * scale, 0, false);
+                p = __builtin_amdgcn_cvt_pk_fp8_f32(__uint_as_float(b << 16) * scale, __uint_as_float(b & 0xFFFF0000u) * scale, p, true);
+                packed[half] = uint32_t(p);
+            }
+            codes[j * kWave + lane] = u32x2{packed[0], packed[1]};
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint32_t packed[2];
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                const uint32_t a = words[j][2 * half], b = words[j][2 * half + 1];
+                packed[half] = encode_e4m3(a & 0xFFFFu, shift) | (encode_e4m3(a >> 16, shift) << 8) |
+                               (encode_e4m3(b & 0xFFFFu, shift) << 16) | (encode_e4m3(b >> 16, shift) << 24);
+            }
+            codes[j * kWave + lane] = u32x2{packed[0], packed[1]};
+        }
+    }
+    if (lane == 0) *reinterpret_cast<int16_t*>(out + block_elems + 2ull * g) = int16_t(shift);
+}
+
+__global__ __launch_bounds__(kWave* kCodecWaves) void dequantize_groups_2048(const uint8_t* __restrict__ stage,
+                                                                           const int32_t* __restrict__ ids, uint16_t* __restrict__ pool,
+                                                                           uint32_t count, uint32_t groups_per_block) {
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint64_t group = uint64_t(blockIdx.x) * kCodecWaves + threadIdx.x / kWave;
+    if (group >= uint64_t(count) * groups_per_block) return;
+    const uint32_t index = uint32_t(group / groups_per_block);
+    const uint32_t g = uint32_t(group % groups_per_block);
+    const uint64_t block_elems = uint64_t(kFastGroup) * groups_per_block;
+    const uint64_t record = block_elems + 2ull * groups_per_block;
+    const uint8_t* in = stage + uint64_t(index) * record;
+    const int32_t shift = *reinterpret_cast<const int16_t*>(in + block_elems + 2ull * g);
+    const u32x2* codes = reinterpret_cast<const u32x2*>(in + uint64_t(g) * kFastGroup);
+    u32x4* target = reinterpret_cast<u32x4*>(pool + uint64_t(ids[index]) * block_elems + uint64_t(g) * kFastGroup);
+
+    u32x2 bytes[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bytes[j] = __builtin_nontemporal_load(codes + j * kWave + lane);
+
+    // A byte 0x7F or 0xFF (NaN) becomes 0x80 after masking off its sign and adding one.
+    uint32_t flags = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) flags |= ((bytes[j][0] & 0x7F7F7F7Fu) + 0x01010101u) | ((bytes[j][1] & 0x7F7F7F7Fu) + 0x01010101u);
+    const bool any_nan = __any((flags & 0x80808080u) != 0);
+
+    if (!any_nan && shift >= -117 && shift <= 119) {
+        const float scale = power_of_two(shift);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            u32x4 out;
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {
+                const int word = int(bytes[j][w]);
+                const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(word, false);
+                const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(word, true);
+                out[2 * w] = __builtin_amdgcn_perm(__float_as_uint(lo.y * scale), __float_as_uint(lo.x * scale), 0x07060302u);
+                out[2 * w + 1] = __builtin_amdgcn_perm(__float_as_uint(hi.y * scale), __float_as_uint(hi.x * scale), 0x07060302u);
+            }
+            target[j * kWave + lane] = out;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            u32x4 out;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const uint32_t word = bytes[j][w / 2] >> (16 * (w % 2));
+                out[w] = decode_e4m3(word & 0xFFu, shift) | (decode_e4m3((word >> 8) & 0xFFu, shift) << 16);
+            }
+            target[j * kWave + lane] = out;
+        }
+    }
+}
+
+void launch_quantize_2048(const uint16_t* pool, const int32_t* ids, uint8_t* stage, uint32_t count, uint32_t groups_per_block,
+                          uint32_t grid, hipStream_t stream) {
+    hipLaunchKernelGGL(quantize_groups_2048, dim3(grid), dim3(kWave * kCodecWaves), 0, stream, pool, ids, stage, count, groups_per_block);
+}
+
+void launch_dequantize_2048(const uint8_t* stage, const int32_t* ids, uint16_t* pool, uint32_t count, uint32_t groups_per_block,
+                            uint32_t grid, hipStream_t stream) {
+    hipLaunchKernelGGL(dequantize_groups_2048, dim3(grid), dim3(kWave * kCodecWaves), 0, stream, stage, ids, pool, count, groups_per_block);
+}
+
+}  // namespace lk

@@ -174,8 +174,7 @@ LK_EXPORT int lk_fp8_quantize(const void* pool, const int32_t* ids, uint32_t cou
         const dim3 block(lk::kWave * lk::kCodecWaves);
         auto s = static_cast<hipStream_t>(stream);
         if (lk::fast_records(pool, stage, group_elems, groups_per_block))
-            hipLaunchKernelGGL(lk::quantize_groups_2048, dim3(grid), block, 0, s, static_cast<const uint16_t*>(pool), ids,
-                               static_cast<uint8_t*>(stage), count, groups_per_block);
+            lk::launch_quantize_2048(static_cast<const uint16_t*>(pool), ids, static_cast<uint8_t*>(stage), count, groups_per_block, grid, s);
         else
             hipLaunchKernelGGL(lk::quantize_groups_any, dim3(grid), block, 0, s, static_cast<const uint16_t*>(pool), ids,
                                static_cast<uint8_t*>(stage), count, group_elems, groups_per_block);
@@ -192,8 +191,7 @@ LK_EXPORT int lk_fp8_dequantize(const void* stage, const int32_t* ids, uint32_t 
         const dim3 block(lk::kWave * lk::kCodecWaves);
         auto s = static_cast<hipStream_t>(stream);
         if (lk::fast_records(pool, stage, group_elems, groups_per_block))
-            hipLaunchKernelGGL(lk::dequantize_groups_2048, dim3(grid), block, 0, s, static_cast<const uint8_t*>(stage), ids,
-                               static_cast<uint16_t*>(pool), count, groups_per_block);
+            lk::launch_dequantize_2048(static_cast<const uint8_t*>(stage), ids, static_cast<uint16_t*>(pool), count, groups_per_block, grid, s);
         else
             hipLaunchKernelGGL(lk::dequantize_groups_any, dim3(grid), block, 0, s, static_cast<const uint8_t*>(stage), ids,
                                static_cast<uint16_t*>(pool), count, group_elems, groups_per_block);

@@ -105,6 +105,74 @@ def test_records_are_bit_exact_and_restore_bit_exact(fp8, shape):
     assert np.array_equal(restored.view(torch.int16).cpu().numpy().view(np.uint16), reference)
 
 
+def crafted_groups(group=2048):
+    """Groups that reach every finite BF16 pattern at every shift the computed scale can take:
+    for each largest exponent m (shift m - 134), one pinned 2^(m-127) followed by every
+    pattern whose exponent is at most m, zero-padded (zeros leave the shift unchanged)."""
+    raw = (ALL_BF16 >> 7) & 0xFF
+    groups = []
+    for m in range(1, 255):
+        patterns = ALL_BF16[(raw <= m)]
+        per = group - 1
+        for start in range(0, patterns.size, per):
+            chunk = patterns[start : start + per]
+            g = np.zeros(group, dtype=np.uint16)
+            g[0] = m << 7
+            g[1 : 1 + chunk.size] = chunk
+            groups.append(g)
+    # Groups with infinities and NaN (the exact fallback), and all-zero / all-subnormal groups.
+    for special in ([0x7F80, 0x3F80, 0xBC00], [0xFF80, 0x0001, 0x8005], [0x7FC1, 0x4000], [0x0000], [0x0001, 0x807F, 0x8000]):
+        g = np.resize(np.array(special, dtype=np.uint16), group)
+        groups.append(g)
+    return np.stack(groups)
+
+
+def test_record_fast_paths_are_bit_exact_for_every_pattern_at_every_shift(fp8):
+    groups = crafted_groups()
+    per_block = 576
+    blocks = -(-groups.shape[0] // per_block)
+    bits = np.zeros((blocks * per_block, 2048), dtype=np.uint16)
+    bits[: groups.shape[0]] = groups
+    bits = bits.reshape(blocks, -1)
+    layout = fp8.Fp8Layout(2048, per_block)
+    ids = np.arange(blocks, dtype=np.int32)[::-1].copy()
+    expected = oracle.quantize_records(bits, ids, layout.group_elems, layout.groups_per_block)
+    pool = torch.from_numpy(bits.view(np.int16)).cuda().view(torch.bfloat16)
+    stage = torch.zeros(expected.size, dtype=torch.uint8, device="cuda")
+    fp8.quantize_blocks(pool, torch.from_numpy(ids).cuda(), stage, layout)
+    got = stage.cpu().numpy()
+    mismatch = np.flatnonzero(got != expected)
+    assert mismatch.size == 0, f"{mismatch.size} bytes differ, first at {mismatch[:4]}"
+    restored = torch.zeros_like(pool)
+    fp8.dequantize_blocks(stage, torch.from_numpy(ids).cuda(), restored, layout)
+    reference = np.zeros_like(bits)
+    oracle.dequantize_records(expected, ids, reference, layout.group_elems, layout.groups_per_block)
+    assert np.array_equal(restored.view(torch.int16).cpu().numpy().view(np.uint16), reference)
+
+
+def test_dequantize_fast_path_is_bit_exact_for_every_code_at_every_shift(fp8):
+    per_block = 576
+    layout = fp8.Fp8Layout(2048, per_block)
+    shifts = np.arange(-140, 128)
+    finite = ALL_FP8[(ALL_FP8 & 0x7F) != 0x7F]
+    groups = [np.resize(finite, 2048) for _ in shifts] + [np.resize(ALL_FP8, 2048) for _ in shifts]
+    all_shifts = np.concatenate([shifts, shifts]).astype(np.int16)
+    blocks = -(-len(groups) // per_block)
+    data = np.zeros((blocks * per_block, 2048), dtype=np.uint8)
+    data[: len(groups)] = np.stack(groups)
+    header = np.zeros(blocks * per_block, dtype=np.int16)
+    header[: len(groups)] = all_shifts
+    records = np.concatenate([data.reshape(blocks, -1), header.reshape(blocks, per_block).view(np.uint8)], axis=1).reshape(-1)
+    ids = np.arange(blocks, dtype=np.int32)
+    reference = np.zeros((blocks, layout.block_elems), dtype=np.uint16)
+    oracle.dequantize_records(records, ids, reference, layout.group_elems, layout.groups_per_block)
+    pool = torch.zeros(blocks, layout.block_elems, dtype=torch.bfloat16, device="cuda")
+    fp8.dequantize_blocks(torch.from_numpy(records).cuda(), torch.from_numpy(ids).cuda(), pool, layout)
+    got = pool.view(torch.int16).cpu().numpy().view(np.uint16)
+    mismatch = np.flatnonzero(got != reference)
+    assert mismatch.size == 0, f"{mismatch.size} values differ, first at {mismatch[:4]}"
+
+
 def test_records_address_past_4_gib(fp8):
     layout = fp8.Fp8Layout(2048, 576)
     block_bytes = 2 * layout.block_elems
