@@ -189,10 +189,71 @@ __device__ __forceinline__ bool shift_is_exact_in_fp32(int32_t shift) { return s
 
 __device__ __forceinline__ float pow2(int32_t e) { return __uint_as_float(uint32_t(e + 127) << 23); }
 
+// One (block, KV head) unit of a wave: the lane's share of the K and V tiles and, for FP8,
+// the two group shifts.
+template <int KV>
+struct Tile {
+    SlotRaw<KV> k[2];
+    SlotRaw<KV> v[2];
+    static constexpr int32_t k_shift = 0, v_shift = 0;
+};
+template <>
+struct Tile<LK_FP8_RECORD> {
+    SlotRaw<LK_FP8_RECORD> k[2];
+    SlotRaw<LK_FP8_RECORD> v[2];
+    int32_t k_shift, v_shift;
+};
+
+// BF16 pairs of a lane's 16 K values: BF16 tiles as loaded; FP8 codes by the exact hardware
+// convert (every E4M3 value is a BF16 value), or, for groups whose shift can leave BF16's
+// normal range, by the reference's integer decode with the shift applied.
+template <int KV>
+__device__ __forceinline__ void slot_bf16_pairs(const SlotRaw<KV>& raw, uint32_t (&pairs)[8], bool exact, int32_t shift) {
+    if constexpr (KV == LK_BF16) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pairs[i] = raw.w[i];
+    } else if constexpr (KV == LK_FP8_RECORD) {
+        if (!exact) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                pairs[2 * i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw.w[i], 1.0f, false));
+                pairs[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(raw.w[i], 1.0f, true));
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t word = raw.w[i] >> (16 * h);
+                    pairs[2 * i + h] = decode_e4m3(word & 0xFFu, shift) | (decode_e4m3((word >> 8) & 0xFFu, shift) << 16);
+                }
+            }
+        }
+    }
+}
+
+// Register buffers per wave (see the main loop of decode_split_fast).
+#ifndef LK_DECODE_RING_BF16
+#define LK_DECODE_RING_BF16 2
+#endif
+template <int KV>
+struct RingDepth {
+    static constexpr int value = KV == LK_BF16 ? LK_DECODE_RING_BF16 : 3;
+};
+#ifdef LK_DECODE_TWO_WAVES
+#define LK_DECODE_OCCUPANCY __attribute__((amdgpu_waves_per_eu(2)))
+#else
+#define LK_DECODE_OCCUPANCY
+#endif
+
 template <int KV, int QF, int G>
-__global__ __launch_bounds__(kWave* kDecodeWaves) void decode_split_fast(DecodeArgs a) {
+__global__ __launch_bounds__(kWave* kDecodeWaves) LK_DECODE_OCCUPANCY void decode_split_fast(DecodeArgs a) {
     const uint32_t lane = threadIdx.x % kWave;
-    const uint32_t wave = threadIdx.x / kWave;
+    // Wave-uniform by construction; readfirstlane tells the compiler, so everything derived
+    // from it (block ids, tile addresses' uniform part) goes through scalar loads and
+    // registers. A vector load of a block id would otherwise have to wait for every tile
+    // load in flight before it (loads retire in order), draining the pipeline each unit.
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const uint32_t c = lane % 8;       // dim group
     const uint32_t row = lane / 8;     // slots row and row + 8
     const uint32_t split = blockIdx.x % a.splits;
@@ -207,32 +268,44 @@ __global__ __launch_bounds__(kWave* kDecodeWaves) void decode_split_fast(DecodeA
     const uint32_t count = min(a.bps, nblocks - first);
 
     // q for the G heads of this KV head, this lane's 16 dims, in FP32; BF16 q also packed.
+    // The lane's dims are runs of 8 (BF16 tiles) or 16 (FP8) consecutive ones: 16-byte loads.
     float qf[G][16];
     uint32_t qp[G][8];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-        const uint32_t qh = kv_head * G + h;
+        const uint64_t row_at = (uint64_t(seq) * a.query_heads + kv_head * G + h) * kDim;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const uint64_t at = (uint64_t(seq) * a.query_heads + qh) * kDim + lane_dim<KV>(c, j);
+        for (int run = 0; run < 2; ++run) {
+            const uint32_t d0 = lane_dim<KV>(c, 8 * run);
             if constexpr (QF == LK_BF16) {
-                const uint32_t bits = reinterpret_cast<const uint16_t*>(a.q)[at];
-                qf[h][j] = __uint_as_float(bits << 16);
-            } else {
-                qf[h][j] = reinterpret_cast<const float*>(a.q)[at];
-            }
-        }
+                const u32x4 w = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(a.q) + row_at + d0);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            qp[h][i] = (__float_as_uint(qf[h][2 * i]) >> 16) | (__float_as_uint(qf[h][2 * i + 1]) & 0xFFFF0000u);
+                for (int i = 0; i < 4; ++i) {
+                    qp[h][4 * run + i] = w[i];
+                    qf[h][8 * run + 2 * i] = bf16_lo(w[i]);
+                    qf[h][8 * run + 2 * i + 1] = bf16_hi(w[i]);
+                }
+            } else {
+                const float* src = reinterpret_cast<const float*>(a.q) + row_at + d0;
+#pragma unroll
+                for (int quarter = 0; quarter < 2; ++quarter) {
+                    const u32x4 w = *reinterpret_cast<const u32x4*>(src + 4 * quarter);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) qf[h][8 * run + 4 * quarter + i] = __uint_as_float(w[i]);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    qp[h][4 * run + i] = (__float_as_uint(qf[h][8 * run + 2 * i]) >> 16) | (__float_as_uint(qf[h][8 * run + 2 * i + 1]) & 0xFFFF0000u);
+            }
         }
     }
 
     constexpr uint32_t kElem = KV == LK_FP8_RECORD ? 1 : (KV == LK_F32 ? 4 : 2);
     const uint64_t tile_bytes = uint64_t(kSlots) * kDim * kElem;
     const uint64_t head_tile = uint64_t(a.layer) * a.kv_heads + kv_head;  // group index of K
-    const uint64_t k_offset = head_tile * tile_bytes;
-    const uint64_t v_offset = (uint64_t(a.layers) * a.kv_heads + head_tile) * tile_bytes;
+    const uint64_t k_offset = head_tile * tile_bytes + uint64_t(row) * kDim * kElem;
+    const uint64_t v_offset = (uint64_t(a.layers) * a.kv_heads + head_tile) * tile_bytes + uint64_t(row) * kDim * kElem;
+    const uint64_t half_offset = 8ull * kDim * kElem;                            // slot row + 8
     const uint64_t block_elems = uint64_t(2) * a.layers * a.kv_heads * kSlots * kDim;  // FP8: shifts follow the data
     const int32_t* row_ids = a.table + uint64_t(seq) * a.table_width + first;
 
@@ -245,57 +318,64 @@ __global__ __launch_bounds__(kWave* kDecodeWaves) void decode_split_fast(DecodeA
         for (int j = 0; j < 16; ++j) acc[h][j] = 0.0f;
     }
 
-    SlotRaw<KV> k_raw[2], v_raw[2];
-    int32_t k_shift = 0, v_shift = 0;
-    auto fetch = [&](uint32_t t) {
-        const uint8_t* base = a.pool + uint64_t(row_ids[t]) * a.block_bytes;
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            load_slot<KV>(k_raw[half], base + k_offset + (row + 8 * half) * kDim * kElem, c);
-            load_slot<KV>(v_raw[half], base + v_offset + (row + 8 * half) * kDim * kElem, c);
+    // The block ids of this wave's units, one per lane (a wave has at most 64 units:
+    // blocks per split <= 256), loaded once before any tile and read back with v_readlane.
+    const uint32_t mine = count > wave ? (count - wave + kDecodeWaves - 1) / kDecodeWaves : 0;
+    const int32_t my_block = lane < mine ? row_ids[wave + lane * kDecodeWaves] : 0;
+    // FP8: the unit's two group shifts, likewise one unit per lane, so no load in the main
+    // loop has to be waited for before the tile loads issued ahead of it.
+    int32_t my_k_shift = 0, my_v_shift = 0;
+    if constexpr (KV == LK_FP8_RECORD) {
+        if (lane < mine) {
+            const int16_t* shifts = reinterpret_cast<const int16_t*>(a.pool + uint64_t(uint32_t(my_block)) * a.block_bytes + block_elems);
+            my_k_shift = shifts[head_tile];
+            my_v_shift = shifts[uint64_t(a.layers) * a.kv_heads + head_tile];
         }
+    }
+
+    auto fetch = [&](Tile<KV>& tile, uint32_t i) {
+        const int32_t block = __builtin_amdgcn_readlane(my_block, i);
+        const uint8_t* base = a.pool + uint64_t(uint32_t(block)) * a.block_bytes;
+        load_slot<KV>(tile.k[0], base + k_offset, c);
+        load_slot<KV>(tile.k[1], base + k_offset + half_offset, c);
+        load_slot<KV>(tile.v[0], base + v_offset, c);
+        load_slot<KV>(tile.v[1], base + v_offset + half_offset, c);
         if constexpr (KV == LK_FP8_RECORD) {
-            const int16_t* shifts = reinterpret_cast<const int16_t*>(base + block_elems);
-            k_shift = shifts[head_tile];
-            v_shift = shifts[uint64_t(a.layers) * a.kv_heads + head_tile];
+            tile.k_shift = __builtin_amdgcn_readlane(my_k_shift, i);
+            tile.v_shift = __builtin_amdgcn_readlane(my_v_shift, i);
         }
     };
 
-    uint32_t t = wave;
-    if (t < count) fetch(t);
-    for (; t < count; t += kDecodeWaves) {
-        SlotRaw<KV> kc[2] = {k_raw[0], k_raw[1]}, vc[2] = {v_raw[0], v_raw[1]};
-        const int32_t ks = k_shift, vs = v_shift;
-        if (t + kDecodeWaves < count) fetch(t + kDecodeWaves);
-
+    // The unit of tile t: scores, online-softmax update, weighted V.
+    auto consume = [&](const Tile<KV>& tile, uint32_t t) {
         const uint32_t token0 = (first + t) * kSlots;
         const bool partial = token0 + kSlots > uint32_t(length);
         const bool visible[2] = {token0 + row < uint32_t(length), token0 + row + 8 < uint32_t(length)};
 
-        // Scores, base 2, for both slots of this lane and every head.
         float score[G][2];
-        bool k_exact = true;
+        bool k_exact = false;
         float k_factor = a.scale_log2;
         if constexpr (KV == LK_FP8_RECORD) {
-            k_exact = !shift_is_exact_in_fp32(ks);
-            if (!k_exact) k_factor *= pow2(ks);
+            k_exact = !shift_is_exact_in_fp32(tile.k_shift);
+            if (!k_exact) k_factor *= pow2(tile.k_shift);
         }
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
             float dot[G];
-            if constexpr (KV == LK_BF16 && QF == LK_BF16) {
+            if constexpr (KV != LK_F32 && QF == LK_BF16) {
+                uint32_t pairs[8];
+                slot_bf16_pairs<KV>(tile.k[half], pairs, k_exact, tile.k_shift);
 #pragma unroll
                 for (int h = 0; h < G; ++h) {
                     float s = 0.0f;
 #pragma unroll
                     for (int i = 0; i < 8; ++i)
-                        s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, kc[half].w[i]),
-                                                            __builtin_bit_cast(bf16x2, qp[h][i]), s, false);
+                        s = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pairs[i]), __builtin_bit_cast(bf16x2, qp[h][i]), s, false);
                     dot[h] = s;
                 }
             } else {
                 float kv[16];
-                unpack_slot<KV>(kc[half], kv, k_exact, ks);
+                unpack_slot<KV>(tile.k[half], kv, k_exact, tile.k_shift);
 #pragma unroll
                 for (int h = 0; h < G; ++h) {
                     float s = 0.0f;
@@ -315,7 +395,9 @@ __global__ __launch_bounds__(kWave* kDecodeWaves) void decode_split_fast(DecodeA
         bool raise = false;
 #pragma unroll
         for (int h = 0; h < G; ++h) raise |= fmaxf(score[h][0], score[h][1]) > m[h] + kRescaleThreshold;
-        if (__any(raise)) {
+        if (__builtin_expect(__any(raise), 0)) {
+            // Kept as a branch: flattened, its multiplies would run on every unit.
+            asm volatile("" ::: "memory");
 #pragma unroll
             for (int h = 0; h < G; ++h) {
                 const float top = fmaxf(score[h][0], score[h][1]);
@@ -328,16 +410,16 @@ __global__ __launch_bounds__(kWave* kDecodeWaves) void decode_split_fast(DecodeA
             }
         }
 
-        bool v_exact = true;
+        bool v_exact = false;
         float v_factor = 1.0f;
         if constexpr (KV == LK_FP8_RECORD) {
-            v_exact = !shift_is_exact_in_fp32(vs);
-            if (!v_exact) v_factor = pow2(vs);
+            v_exact = !shift_is_exact_in_fp32(tile.v_shift);
+            if (!v_exact) v_factor = pow2(tile.v_shift);
         }
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
             float vv[16];
-            unpack_slot<KV>(vc[half], vv, v_exact, vs);
+            unpack_slot<KV>(tile.v[half], vv, v_exact, tile.v_shift);
             if (partial && !visible[half]) {
 #pragma unroll
                 for (int j = 0; j < 16; ++j) vv[j] = 0.0f;
@@ -349,6 +431,28 @@ __global__ __launch_bounds__(kWave* kDecodeWaves) void decode_split_fast(DecodeA
                 const float pv = p * v_factor;
 #pragma unroll
                 for (int j = 0; j < 16; ++j) acc[h][j] = fmaf(pv, vv[j], acc[h][j]);
+            }
+        }
+    };
+
+    // This wave's units are t = wave, wave + 4, ...: a ring of kRing register buffers, each
+    // refilled as soon as it is consumed, keeps kRing - 1 units' loads in flight while one
+    // computes.
+    constexpr int kRing = RingDepth<KV>::value;
+    Tile<KV> ring[kRing];
+    auto unit = [&](uint32_t i) { return wave + i * kDecodeWaves; };
+    // Refills are unconditional: past the wave's last unit they re-read that unit (an L2 hit),
+    // because a conditional load would make every later wait assume it might not have been
+    // issued, i.e. wait for all loads in flight.
+    if (mine > 0) {
+        const uint32_t last = mine - 1;
+#pragma unroll
+        for (int d = 0; d < kRing; ++d) fetch(ring[d], min(uint32_t(d), last));
+        for (uint32_t i = 0; i < mine; i += kRing) {
+#pragma unroll
+            for (int d = 0; d < kRing; ++d) {
+                if (i + d < mine) consume(ring[d], unit(i + d));
+                fetch(ring[d], min(i + d + kRing, last));
             }
         }
     }
@@ -503,19 +607,50 @@ __global__ __launch_bounds__(kWave) void decode_split_generic(DecodeArgs a) {
 
 template <int QF>
 __global__ __launch_bounds__(kWave) void decode_combine(DecodeArgs a, void* out) {
+    const uint32_t lane = threadIdx.x;
     const uint32_t qh = blockIdx.x % a.query_heads;
     const uint32_t seq = blockIdx.x / a.query_heads;
     const uint32_t used = (blocks_of(a.lengths[seq], a.slots) + a.bps - 1) / a.bps;
     const uint64_t base = (uint64_t(seq) * a.query_heads + qh) * a.splits;
+    const float* ml = a.partial_ml + 2 * base;
+
+    // Lanes across splits: the largest running max, then the total weight.
     float top = -INFINITY;
-    for (uint32_t s = 0; s < used; ++s) top = fmaxf(top, a.partial_ml[2 * (base + s)]);
+    for (uint32_t s = lane; s < used; s += kWave) top = fmaxf(top, ml[2 * s]);
+#pragma unroll
+    for (int mask = 32; mask >= 1; mask >>= 1) top = fmaxf(top, __shfl_xor(top, mask, kWave));
     float total = 0.0f;
-    for (uint32_t s = 0; s < used; ++s) total += a.partial_ml[2 * (base + s) + 1] * merge_weight(a.partial_ml[2 * (base + s)], top);
+    for (uint32_t s = lane; s < used; s += kWave) total += ml[2 * s + 1] * merge_weight(ml[2 * s], top);
+#pragma unroll
+    for (int mask = 32; mask >= 1; mask >>= 1) total += __shfl_xor(total, mask, kWave);
     const float inverse = 1.0f / total;
-    for (uint32_t d = threadIdx.x; d < a.head_dim; d += kWave) {
-        float sum = 0.0f;
-        for (uint32_t s = 0; s < used; ++s) sum += a.partial_acc[(base + s) * a.head_dim + d] * merge_weight(a.partial_ml[2 * (base + s)], top);
-        const float value = sum * inverse;
+
+    // Lanes across dims: sum the splits' accumulators, 64 splits' weights at a time, each
+    // broadcast from the lane that computed it.
+    constexpr uint32_t kPer = kMaxGenericDim / kWave;
+    float sum[kPer];
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) sum[i] = 0.0f;
+    const float* acc = a.partial_acc + base * a.head_dim;
+    for (uint32_t chunk = 0; chunk < used; chunk += kWave) {
+        const uint32_t s = chunk + lane;
+        const float weight = s < used ? merge_weight(ml[2 * s], top) : 0.0f;
+        const uint32_t n = min(kWave, used - chunk);
+        for (uint32_t j = 0; j < n; ++j) {
+            const float w = __shfl(weight, j, kWave);
+            const float* row = acc + uint64_t(chunk + j) * a.head_dim;
+#pragma unroll
+            for (uint32_t i = 0; i < kPer; ++i) {
+                const uint32_t d = lane + i * kWave;
+                if (d < a.head_dim) sum[i] = fmaf(w, row[d], sum[i]);
+            }
+        }
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) {
+        const uint32_t d = lane + i * kWave;
+        if (d >= a.head_dim) continue;
+        const float value = sum[i] * inverse;
         const uint64_t at = (uint64_t(seq) * a.query_heads + qh) * a.head_dim + d;
         if constexpr (QF == LK_BF16) reinterpret_cast<uint16_t*>(out)[at] = to_bf16(value);
         else reinterpret_cast<float*>(out)[at] = value;

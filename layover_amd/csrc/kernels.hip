@@ -100,7 +100,8 @@ Geometry geometry(const lk_decode_shape& s, const void* pool = nullptr) {
     // Work units counted per KV head for both kernels, so the split count (and with it the
     // workspace size) does not depend on which kernel runs.
     const uint64_t units = uint64_t(s.batch) * s.kv_heads;
-    uint32_t bps = env_bps();
+    // At most 256 blocks per split: the fast kernel's waves hold their block ids one per lane.
+    uint32_t bps = env_bps() > 256 ? 256 : env_bps();
     if (bps == 0) {
         const uint64_t target = 4096;
         const uint64_t wanted = (units * s.table_width + target - 1) / target;
