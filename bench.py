@@ -111,6 +111,30 @@ def measure_link(device, nbytes: int = 512 << 20, repeats: int = 5) -> dict:
     return out
 
 
+def measure_hbm(device, nbytes: int = 8 << 30, repeats: int = 5) -> dict:
+    """HBM probes on this GPU: a read-only reduction and a device-to-device copy over 8 GiB
+    (torch kernels), the measured ceilings beside the 8 TB/s specification."""
+    import torch
+
+    src = torch.ones(nbytes // 2, dtype=torch.bfloat16, device=device)
+    dst = torch.empty_like(src)
+    out = {}
+    for name, fn, moved in (("read_gbs", lambda: src.sum(dtype=torch.float32), nbytes),
+                            ("copy_gbs", lambda: dst.copy_(src), 2 * nbytes)):
+        fn()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(repeats):
+            fn()
+        end.record()
+        end.synchronize()
+        out[name] = repeats * moved / (start.elapsed_time(end) * 1e-3) / 1e9
+    del src, dst
+    torch.cuda.empty_cache()
+    return out
+
+
 def swap_bench(args, device, pool_blocks: int, cache):
     import numpy as np
     import torch
@@ -325,8 +349,9 @@ def main() -> None:
     fill_pool(cache.pool, seed=0, outlier_fraction=0.001)
     torch.cuda.synchronize()
 
-    log("link probe")
+    log("link and HBM probes")
     link = measure_link(device)
+    hbm = measure_hbm(device)
     swap = swap_bench(args, device, pool_blocks, cache)
     layout = Fp8Layout.from_cache(cache)
     bytes_round_trip = 2 * swap["bytes_each_way"]
@@ -366,6 +391,7 @@ def main() -> None:
             "parity": f"bit-exact vs oracle on {swap['parity_sample_records']} sampled records and their restored blocks",
             "segments_per_direction": swap["segments_per_direction"],
         },
+        "hbm_probe": {k: round(v, 1) for k, v in hbm.items()},
         "link": {"d2h_gbs": round(link["d2h_gbs"], 2), "h2d_gbs": round(link["h2d_gbs"], 2), "probe_bytes": link["bytes"],
                  "kind": "pinned hipMemcpyAsync, measured in this run"},
         "roofline": {

@@ -64,13 +64,24 @@ bool fast_records(const void* pool, const void* stage, uint64_t group_elems, uin
 }
 
 // Decode launch geometry: blocks per split (bps) and splits per sequence, from the shape only.
-// Enough workgroups to keep all 256 CUs busy at the widest table (about 16 per CU at full
-// lengths), but splits of at least 16 blocks so each wave streams several tiles.
+// About 16 workgroups per CU if every row used the whole table width (so about 8 at the
+// typical half-full width of mixed lengths), with splits of 64 to 256 blocks: shorter splits
+// spend more on each workgroup's q load and state merge and on the combine pass than they
+// gain in balance (measured on MI355X: batch 1 at 32k tokens, 16-block splits 92 us per
+// layer, 64-block splits 38 us).
 struct Geometry {
     uint32_t bps;
     uint32_t splits;
     bool fast;
 };
+
+uint32_t env_heads_inner() {
+    static const uint32_t value = [] {
+        const char* text = getenv("LAYOVER_DECODE_HEADS_INNER");
+        return text ? uint32_t(strtoul(text, nullptr, 10)) : 1u;
+    }();
+    return value;
+}
 
 uint32_t env_bps() {
     static const uint32_t value = [] {
@@ -86,12 +97,13 @@ uint64_t pool_block_bytes(const lk_decode_shape& s) {
     return elems * (s.kv_format == LK_F32 ? 4 : 2);
 }
 
-// The fast kernel needs the Qwen3 tile shape, a supported GQA ratio, and 16-byte aligned
-// tiles (pool base and block stride); anything else runs the generic kernel.
+// The matrix-core kernel needs the Qwen3 tile shape (16 slots x 128 dims), at most 16 query
+// heads per KV head, a BF16 or FP8-record pool and 16-byte aligned tiles (pool base and block
+// stride); anything else runs the generic kernel.
 bool fast_decode(const lk_decode_shape& s, const void* pool) {
     const uint32_t groups = s.query_heads / s.kv_heads;
-    return s.slots == kSlots && s.head_dim == kDim && (groups == 1 || groups == 2 || groups == 4 || groups == 8) &&
-           aligned(pool, 16) && pool_block_bytes(s) % 16 == 0;
+    return s.slots == kSlots && s.head_dim == kDim && groups <= kMaxHeads && s.kv_format != LK_F32 && aligned(pool, 16) &&
+           pool_block_bytes(s) % 16 == 0;
 }
 
 Geometry geometry(const lk_decode_shape& s, const void* pool = nullptr) {
@@ -105,7 +117,7 @@ Geometry geometry(const lk_decode_shape& s, const void* pool = nullptr) {
     if (bps == 0) {
         const uint64_t target = 4096;
         const uint64_t wanted = (units * s.table_width + target - 1) / target;
-        bps = 16;
+        bps = 64;
         while (bps < wanted && bps < 256) bps *= 2;
     }
     g.bps = bps;
@@ -130,24 +142,15 @@ uint64_t workspace_bytes(const lk_decode_shape& s) {
     return uint64_t(s.batch) * s.query_heads * g.splits * (uint64_t(s.head_dim) + 2) * sizeof(float);
 }
 
-template <int KV, int QF>
-void launch_fast(const DecodeArgs& a, uint32_t grid, hipStream_t stream) {
-    switch (a.groups) {
-        case 1: hipLaunchKernelGGL((decode_split_fast<KV, QF, 1>), dim3(grid), dim3(kWave * kDecodeWaves), 0, stream, a); break;
-        case 2: hipLaunchKernelGGL((decode_split_fast<KV, QF, 2>), dim3(grid), dim3(kWave * kDecodeWaves), 0, stream, a); break;
-        case 4: hipLaunchKernelGGL((decode_split_fast<KV, QF, 4>), dim3(grid), dim3(kWave * kDecodeWaves), 0, stream, a); break;
-        default: hipLaunchKernelGGL((decode_split_fast<KV, QF, 8>), dim3(grid), dim3(kWave * kDecodeWaves), 0, stream, a); break;
-    }
-}
-
 template <int QF>
 void launch_decode(const DecodeArgs& a, const Geometry& g, int kv, void* out, hipStream_t stream) {
     if (g.fast) {
         const uint64_t grid = uint64_t(a.batch) * a.kv_heads * g.splits;
         require(grid <= 0x7FFFFFFFull, "decode grid too large");
-        if (kv == LK_BF16) launch_fast<LK_BF16, QF>(a, uint32_t(grid), stream);
-        else if (kv == LK_F32) launch_fast<LK_F32, QF>(a, uint32_t(grid), stream);
-        else launch_fast<LK_FP8_RECORD, QF>(a, uint32_t(grid), stream);
+        if (kv == LK_BF16)
+            hipLaunchKernelGGL((decode_split_mfma<LK_BF16, QF>), dim3(uint32_t(grid)), dim3(kWave * kDecodeWaves), 0, stream, a);
+        else
+            hipLaunchKernelGGL((decode_split_mfma<LK_FP8_RECORD, QF>), dim3(uint32_t(grid)), dim3(kWave * kDecodeWaves), 0, stream, a);
     } else {
         const uint64_t grid = uint64_t(a.batch) * a.query_heads * g.splits;
         require(grid <= 0x7FFFFFFFull, "decode grid too large");
@@ -257,6 +260,7 @@ LK_EXPORT int lk_paged_decode(const lk_decode_shape* shape, const void* q, const
         a.groups = s.query_heads / s.kv_heads;
         a.splits = g.splits;
         a.bps = g.bps;
+        a.heads_inner = lk::env_heads_inner();
         a.block_bytes = lk::pool_block_bytes(s);
         a.scale_log2 = s.scale * lk::kLog2e;
         lk::require(lk::aligned(pool, s.kv_format == LK_F32 ? 4 : (s.kv_format == LK_BF16 ? 2 : 1)), "misaligned pool");
