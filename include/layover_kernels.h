@@ -91,6 +91,12 @@ uint64_t lk_paged_decode_workspace(const lk_decode_shape* shape);
 int lk_paged_decode(const lk_decode_shape* shape, const void* q, const void* pool, const int32_t* table,
                     const int32_t* lengths, void* out, void* workspace, uint64_t workspace_bytes, void* stream);
 
+/* Measurement support, no reference counterpart: stream `bytes` (a multiple of 16, 16-byte
+ * aligned) from `src`, copying to `dst`, or only reading when dst is null (then `sink`, one
+ * device uint32, is written only if the data hash to a value chosen never to occur). This is
+ * the HBM ceiling bench.py reports beside the 8 TB/s specification. */
+int lk_stream_probe(const void* src, void* dst, uint64_t bytes, uint32_t* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -594,8 +594,10 @@ __global__ __launch_bounds__(kWave) void decode_combine(DecodeArgs a, void* out)
     const float inverse = 1.0f / total;
 
     // Lanes across dims: sum the splits' accumulators, 64 splits' weights at a time, each
-    // broadcast from the lane that computed it.
+    // broadcast from the lane that computed it. Rows are read eight at a time, so eight loads
+    // are in flight per lane instead of one round trip per split.
     constexpr uint32_t kPer = kMaxGenericDim / kWave;
+    constexpr uint32_t kBatch = 8;
     float sum[kPer];
 #pragma unroll
     for (uint32_t i = 0; i < kPer; ++i) sum[i] = 0.0f;
@@ -604,13 +606,23 @@ __global__ __launch_bounds__(kWave) void decode_combine(DecodeArgs a, void* out)
         const uint32_t s = chunk + lane;
         const float weight = s < used ? merge_weight(ml[2 * s], top) : 0.0f;
         const uint32_t n = min(kWave, used - chunk);
-        for (uint32_t j = 0; j < n; ++j) {
-            const float w = __shfl(weight, j, kWave);
-            const float* row = acc + uint64_t(chunk + j) * a.head_dim;
+        for (uint32_t j0 = 0; j0 < n; j0 += kBatch) {
+            float rows[kBatch][kPer];
 #pragma unroll
-            for (uint32_t i = 0; i < kPer; ++i) {
-                const uint32_t d = lane + i * kWave;
-                if (d < a.head_dim) sum[i] = fmaf(w, row[d], sum[i]);
+            for (uint32_t u = 0; u < kBatch; ++u) {
+                // Past the last split, re-read it with weight zero rather than branch.
+                const float* row = acc + uint64_t(chunk + min(j0 + u, n - 1)) * a.head_dim;
+#pragma unroll
+                for (uint32_t i = 0; i < kPer; ++i) {
+                    const uint32_t d = lane + i * kWave;
+                    rows[u][i] = d < a.head_dim ? row[d] : 0.0f;
+                }
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < kBatch; ++u) {
+                const float w = __shfl(weight, int(min(j0 + u, kWave - 1)), kWave) * (j0 + u < n ? 1.0f : 0.0f);
+#pragma unroll
+                for (uint32_t i = 0; i < kPer; ++i) sum[i] = fmaf(w, rows[u][i], sum[i]);
             }
         }
     }

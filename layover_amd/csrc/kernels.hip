@@ -161,6 +161,30 @@ void launch_decode(const DecodeArgs& a, const Geometry& g, int kv, void* out, hi
     hipLaunchKernelGGL((decode_combine<QF>), dim3(a.batch * a.query_heads), dim3(kWave), 0, stream, a, out);
 }
 
+// Streaming probe: grid-stride over 16-byte words, four loads in flight per lane.
+__global__ __launch_bounds__(256) void stream_probe(const u32x4* __restrict__ src, u32x4* __restrict__ dst, uint64_t words,
+                                                    uint32_t* __restrict__ sink) {
+    const uint64_t stride = uint64_t(gridDim.x) * blockDim.x;
+    uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    uint32_t hash = 0;
+    for (; i + 3 * stride < words; i += 4 * stride) {
+        u32x4 w[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w[k] = __builtin_nontemporal_load(src + i + k * stride);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if (dst) __builtin_nontemporal_store(w[k], dst + i + k * stride);
+            hash ^= w[k][0] ^ w[k][1] ^ w[k][2] ^ w[k][3];
+        }
+    }
+    for (; i < words; i += stride) {
+        const u32x4 w = src[i];
+        if (dst) dst[i] = w;
+        hash ^= w[0] ^ w[1] ^ w[2] ^ w[3];
+    }
+    if (hash == 0x9E3779B9u) *sink = hash;
+}
+
 }  // namespace lk
 
 #define LK_EXPORT extern "C" __attribute__((visibility("default")))
@@ -267,5 +291,19 @@ LK_EXPORT int lk_paged_decode(const lk_decode_shape* shape, const void* q, const
         auto st = static_cast<hipStream_t>(stream);
         if (s.q_format == LK_BF16) lk::launch_decode<LK_BF16>(a, g, s.kv_format, out, st);
         else lk::launch_decode<LK_F32>(a, g, s.kv_format, out, st);
+    });
+}
+
+LK_EXPORT int lk_stream_probe(const void* src, void* dst, uint64_t bytes, uint32_t* sink, void* stream) {
+    return lk::guarded([&] {
+        lk::require(src != nullptr && sink != nullptr, "null src or sink");
+        lk::require(bytes % 16 == 0 && lk::aligned(src, 16) && (dst == nullptr || lk::aligned(dst, 16)), "16-byte granularity required");
+        if (bytes == 0) return;
+        int device = 0, units = 0;
+        (void)hipGetDevice(&device);
+        (void)hipDeviceGetAttribute(&units, hipDeviceAttributeMultiprocessorCount, device);
+        const uint32_t grid = uint32_t((units > 0 ? units : 256) * 8);
+        hipLaunchKernelGGL(lk::stream_probe, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
+                           static_cast<const lk::u32x4*>(src), static_cast<lk::u32x4*>(dst), bytes / 16, sink);
     });
 }
