@@ -293,6 +293,169 @@ def decode_bench(device, pool, lengths, steps: int, warmup: int, seed: int, dist
     }
 
 
+def decode_step_events(device, pool, table, lens, q, out, workspace, groups):
+    """Launch one decode step (36 single-layer launches) on the current stream, bracketed by
+    timing events; returns the events."""
+    import torch
+
+    from layover_amd.kernels import hip_decode
+
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for layer in range(QWEN["layers"]):
+        hip_decode.run_kernel(q, pool, layer, table, lens, groups, out, workspace)
+    end.record()
+    return start, end
+
+
+def overlap_bench(device, cache, pool_blocks: int, swap_blocks: int = 2048) -> dict:
+    """decode steps (batch 32, mixed contexts, BF16) on torch's stream
+    while an FP8 swap of 2,048 blocks (32,768 tokens) runs on the backend's streams, then the
+    swap-in. Decode reads blocks [0, pool - 2048); the swap reads from there and writes into
+    the last 2048 blocks, so no decode step reads a block being restored."""
+    import numpy as np
+    import torch
+
+    from layover_amd.kernels import hip_decode
+    from layover_amd.kv.transfer import NativeBackend
+
+    rng = np.random.default_rng(7)
+    decode_region = pool_blocks - swap_blocks
+    lengths = [int(n) for n in rng.integers(1024, 32769, size=32)]
+    table = torch.from_numpy(decode_tables(rng, 32, lengths, decode_region, False)).to(device)
+    lens = torch.tensor(lengths, dtype=torch.int32, device=device)
+    q = torch.randn(32, QWEN["query_heads"], QWEN["head_dim"], device=device).to(torch.bfloat16)
+    out = torch.empty_like(q)
+    groups = QWEN["query_heads"] // QWEN["kv_heads"]
+    shape = hip_decode.decode_shape(q, cache.pool, 0, table, groups)
+    workspace = torch.empty(hip_decode.workspace_bytes(shape), dtype=torch.uint8, device=device)
+    step = lambda: decode_step_events(device, cache.pool, table, lens, q, out, workspace, groups)
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    solo = [step() for _ in range(5)]
+    torch.cuda.synchronize()
+    solo_ms = sum(s.elapsed_time(e) for s, e in solo) / len(solo)
+
+    src = [int(i) for i in rng.choice(decode_region, swap_blocks, replace=False)]
+    dst = list(range(decode_region, pool_blocks))
+    backend = NativeBackend(device, staging_bytes=128 << 20, num_staging=2, ids_capacity=1 << 20)
+    backend.prepare(cache, fp8=True)
+    warm = backend.start_out(cache, src[:256], fp8=True)
+    warm.wait()
+    backend.start_in(cache, dst[:256], warm.payload).wait()
+    backend.free(warm.payload)
+    torch.cuda.synchronize()
+
+    def overlapped(start_transfer):
+        """Keep two decode steps queued on the compute stream while the transfer runs, and
+        poll the ticket every ~0.2 ms, so the transfer's end is timed to that resolution."""
+        steps = []
+        t0 = time.perf_counter()
+        ticket = start_transfer()
+        while not ticket.done():
+            pending = [e for _, e in steps[-2:] if not e.query()]
+            if len(pending) < 2:
+                steps.append(step())
+            else:
+                time.sleep(0.0002)
+        elapsed = (time.perf_counter() - t0) * 1e3
+        torch.cuda.synchronize()
+        return ticket, elapsed, steps
+
+    out_ticket, out_ms, out_steps = overlapped(lambda: backend.start_out(cache, src, fp8=True))
+    payload = out_ticket.payload
+    in_ticket, in_ms, in_steps = overlapped(lambda: backend.start_in(cache, dst, payload))
+    torch.cuda.synchronize()
+    during = [s.elapsed_time(e) for s, e in out_steps + in_steps]
+    backend.free(payload)
+    backend.close()
+    record = 1_180_800
+    blocks = sum(-(-n // 16) for n in lengths)
+    kv_bytes = blocks * QWEN["kv_heads"] * 2 * 16 * 128 * 2 * QWEN["layers"]
+    overlap_ms = out_ms + in_ms
+    decode_during_ms = sum(during) / max(1, len(during))
+    return {
+        "decode_step_solo_ms": round(solo_ms, 3),
+        "decode_step_during_swap_ms": round(decode_during_ms, 3),
+        "decode_inflation_pct": round(100 * (decode_during_ms / solo_ms - 1), 1),
+        "decode_steps_during_swap": len(during),
+        "swap_out_ms": round(out_ms, 2),
+        "swap_in_ms": round(in_ms, 2),
+        "swap_blocks": swap_blocks,
+        "pcie_gbs": round(2 * swap_blocks * record / (overlap_ms * 1e-3) / 1e9, 2),
+        "decode_hbm_gbs_during_swap": round(kv_bytes / (decode_during_ms * 1e-3) / 1e9, 1),
+    }
+
+
+def distinct_decode(device, steps: int) -> dict:
+    """The config-3 decode on a pool with one distinct block per table entry (about 80 GB),
+    so no block is read by two sequences: the sensitivity run for the 12 GiB pool's aliasing."""
+    import numpy as np
+    import torch
+
+    rng = np.random.default_rng(2)
+    lengths = [int(n) for n in rng.integers(1024, 32769, size=32)]
+    blocks = sum(-(-n // 16) for n in lengths)
+    pool = torch.empty(blocks, 2, QWEN["layers"], QWEN["kv_heads"], 16, QWEN["head_dim"], dtype=torch.bfloat16, device=device)
+    fill_pool(pool, seed=5)
+    run = decode_bench(device, pool, lengths, steps, 1, seed=3, distinct=True)
+    run["pool_gb"] = round(pool.numel() * 2 / 1e9, 1)
+    del pool
+    torch.cuda.empty_cache()
+    return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in run.items()}
+
+
+def cpu_reference_config1(blocks_in_pool: int = 256, moved: int = 64) -> dict | None:
+    """BASELINE configs[0] on the host: the reference's own host transfer library (built from
+    its sources into oracle/_ref) gathers 64 random blocks of a BF16 pool into pinned host
+    memory and scatters them into 64 other ids, bit-exact. The pool is 256 blocks rather
+    than 4,096 to bound the fill time; per-block work does not depend on the pool size."""
+    import numpy as np
+
+    from layover_amd.kv.native import Engine
+    from oracle import oracle
+
+    if not oracle.REFERENCE_LIBRARY.exists():
+        return None
+    block = 2_359_296
+    rng = np.random.default_rng(0)
+    pool = oracle.bf16_bits(rng.standard_normal(blocks_in_pool * block // 2, dtype=np.float32)).view(np.uint8)
+    order = rng.permutation(blocks_in_pool)
+    src, dst = [int(i) for i in order[:moved]], [int(i) for i in order[moved : 2 * moved]]
+    expected = oracle.gather(pool, block, src)
+    engine = Engine("host", staging_bytes=128 << 20, ids_capacity=1 << 16, library=oracle.REFERENCE_LIBRARY)
+    try:
+        host = engine.host_alloc(moved * block)
+        times = {}
+        for name, call, ids in (("out", engine.out_gather, src), ("in", engine.in_scatter, dst)):  # untimed: first touch of pages
+            transfer = call(pool.ctypes.data, block, ids, host)
+            engine.wait(transfer)
+            engine.release(transfer)
+        for name, call, ids in (("out", engine.out_gather, src), ("in", engine.in_scatter, dst)):
+            t0 = time.perf_counter()
+            transfer = call(pool.ctypes.data, block, ids, host)
+            engine.wait(transfer)
+            times[name] = time.perf_counter() - t0
+            engine.release(transfer)
+        ok = np.array_equal(oracle.gather(pool, block, dst), expected)
+    finally:
+        engine.destroy()
+    moved_bytes = moved * block
+    return {
+        "out_ms": round(times["out"] * 1e3, 2),
+        "in_ms": round(times["in"] * 1e3, 2),
+        "out_gbs": round(moved_bytes / times["out"] / 1e9, 2),
+        "in_gbs": round(moved_bytes / times["in"] / 1e9, 2),
+        "bytes_each_way": moved_bytes,
+        "bit_exact": bool(ok),
+        "threads": 2,
+        "kind": "reference",
+        "sample": f"reference host flavour (oracle/_ref), {moved} of {blocks_in_pool} Qwen3-4B BF16 blocks out then into {moved} other ids",
+    }
+
+
 def cpu_baseline(layout, blocks_sample: int) -> dict:
     """The oracle's single-threaded C FP8 quantize + dequantize over a sample of blocks, scaled
     to the 512-block workload."""
@@ -335,6 +498,8 @@ def main() -> None:
     parser.add_argument("--skip-decode", action="store_true")
     parser.add_argument("--skip-cpu", action="store_true")
     parser.add_argument("--cpu-blocks", type=int, default=64)
+    parser.add_argument("--skip-overlap", action="store_true")
+    parser.add_argument("--skip-distinct", action="store_true")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this KV data path has no multi-GPU step (--gpus {args.gpus} refused)", file=sys.stderr)
@@ -439,6 +604,13 @@ def main() -> None:
         del records, fp8_pool
         torch.cuda.empty_cache()
 
+    if not args.skip_decode and not args.skip_overlap:
+        log("overlap: decode during a 2,048-block FP8 swap (config 5)")
+        result["overlap"] = overlap_bench(device, cache, pool_blocks)
+    if not args.skip_decode and not args.skip_distinct:
+        log("decode on distinct blocks (~80 GB pool)")
+        result["decode_distinct"] = distinct_decode(device, args.decode_steps)
+
     # Last, so its 12 GiB of buffers come and go after everything timed above.
     log("HBM probe")
     result["hbm_probe"] = {k: round(v, 1) for k, v in measure_hbm(device).items()}
@@ -455,6 +627,11 @@ def main() -> None:
             "kind": "port",
             "sample": f"oracle C quantize+dequantize of {cpu['blocks']} Qwen3-4B blocks ({cpu['seconds']:.2f} s), scaled to {args.blocks} blocks; arithmetic only, no host copies",
         }
+    if not args.skip_cpu:
+        log("config 1: reference host library, BF16 gather/scatter")
+        reference = cpu_reference_config1()
+        if reference is not None:
+            result["cpu_reference_config1"] = reference
     calibrate_copy(device)
     print(json.dumps(result), flush=True)
 

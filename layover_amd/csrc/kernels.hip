@@ -161,19 +161,23 @@ void launch_decode(const DecodeArgs& a, const Geometry& g, int kv, void* out, hi
     hipLaunchKernelGGL((decode_combine<QF>), dim3(a.batch * a.query_heads), dim3(kWave), 0, stream, a, out);
 }
 
-// Streaming probe: grid-stride over 16-byte words, four loads in flight per lane.
+// Streaming probe: grid-stride over 16-byte words, kUnroll loads in flight per lane.
+template <bool kNontemporal, int kUnroll>
 __global__ __launch_bounds__(256) void stream_probe(const u32x4* __restrict__ src, u32x4* __restrict__ dst, uint64_t words,
                                                     uint32_t* __restrict__ sink) {
     const uint64_t stride = uint64_t(gridDim.x) * blockDim.x;
     uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     uint32_t hash = 0;
-    for (; i + 3 * stride < words; i += 4 * stride) {
-        u32x4 w[4];
+    for (; i + (kUnroll - 1) * stride < words; i += kUnroll * stride) {
+        u32x4 w[kUnroll];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) w[k] = __builtin_nontemporal_load(src + i + k * stride);
+        for (int k = 0; k < kUnroll; ++k) w[k] = kNontemporal ? __builtin_nontemporal_load(src + i + k * stride) : src[i + k * stride];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            if (dst) __builtin_nontemporal_store(w[k], dst + i + k * stride);
+        for (int k = 0; k < kUnroll; ++k) {
+            if (dst) {
+                if (kNontemporal) __builtin_nontemporal_store(w[k], dst + i + k * stride);
+                else dst[i + k * stride] = w[k];
+            }
             hash ^= w[k][0] ^ w[k][1] ^ w[k][2] ^ w[k][3];
         }
     }
@@ -302,8 +306,10 @@ LK_EXPORT int lk_stream_probe(const void* src, void* dst, uint64_t bytes, uint32
         int device = 0, units = 0;
         (void)hipGetDevice(&device);
         (void)hipDeviceGetAttribute(&units, hipDeviceAttributeMultiprocessorCount, device);
-        const uint32_t grid = uint32_t((units > 0 ? units : 256) * 8);
-        hipLaunchKernelGGL(lk::stream_probe, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
+        // Non-temporal loads, four in flight per lane, 16 workgroups per CU: the fastest of the
+        // probe variants measured on MI355X (read 6.5 TB/s over 8 GiB).
+        const uint32_t grid = uint32_t((units > 0 ? units : 256) * 16);
+        hipLaunchKernelGGL((lk::stream_probe<true, 4>), dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
                            static_cast<const lk::u32x4*>(src), static_cast<lk::u32x4*>(dst), bytes / 16, sink);
     });
 }
