@@ -88,7 +88,7 @@ struct DecodeArgs {
     uint32_t groups;       // query heads per KV head
     uint32_t splits;       // splits per sequence (grid)
     uint32_t bps;          // blocks per split
-    uint32_t heads_inner;  // 1: workgroups ordered (sequence, split, KV head), else (sequence, KV head, split)
+    uint32_t order;        // workgroup order, see decode_unit_of
     uint64_t block_bytes;  // bytes from one pool block to the next
     float scale_log2;      // softmax scale * log2(e)
 };
@@ -177,6 +177,24 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 #define LK_DECODE_RING_FP8 4
 #endif
 
+// Workgroup -> (sequence, split, KV head). Order 1 (the default): KV head fastest, so the
+// eight heads' tiles of a block (adjacent 4 KiB pieces) are read close together in time, by
+// workgroups that the round-robin dealing puts on different XCDs. Order 0: KV head slowest.
+// Measured on MI355X, batch 32 mixed contexts, per layer: order 1 294 us, order 0 419 us, and
+// keeping a block's heads on one XCD instead (so they share its L2) 370 us.
+__device__ __forceinline__ bool decode_unit_of(const DecodeArgs& a, uint32_t w, uint32_t* seq, uint32_t* split, uint32_t* kv_head) {
+    if (a.order == 0) {
+        *split = w % a.splits;
+        *kv_head = (w / a.splits) % a.kv_heads;
+        *seq = w / (a.splits * a.kv_heads);
+    } else {
+        *kv_head = w % a.kv_heads;
+        *split = (w / a.kv_heads) % a.splits;
+        *seq = w / (a.kv_heads * a.splits);
+    }
+    return *seq < a.batch;
+}
+
 template <int KV, int QF>
 __global__ __launch_bounds__(kWave* kDecodeWaves) void decode_split_mfma(DecodeArgs a) {
     const uint32_t lane = threadIdx.x % kWave;
@@ -186,15 +204,7 @@ __global__ __launch_bounds__(kWave* kDecodeWaves) void decode_split_mfma(DecodeA
     const uint32_t g = lane / 16;
     const uint32_t n = lane % 16;
     uint32_t split, kv_head, seq;
-    if (a.heads_inner) {
-        kv_head = blockIdx.x % a.kv_heads;
-        split = (blockIdx.x / a.kv_heads) % a.splits;
-        seq = blockIdx.x / (a.kv_heads * a.splits);
-    } else {
-        split = blockIdx.x % a.splits;
-        kv_head = (blockIdx.x / a.splits) % a.kv_heads;
-        seq = blockIdx.x / (a.splits * a.kv_heads);
-    }
+    if (!decode_unit_of(a, blockIdx.x, &seq, &split, &kv_head)) return;
     const uint32_t groups = a.groups;
 
     const int32_t length = a.lengths[seq];

@@ -75,10 +75,10 @@ struct Geometry {
     bool fast;
 };
 
-uint32_t env_heads_inner() {
+uint32_t env_order() {
     static const uint32_t value = [] {
-        const char* text = getenv("LAYOVER_DECODE_HEADS_INNER");
-        return text ? uint32_t(strtoul(text, nullptr, 10)) : 1u;
+        const char* text = getenv("LAYOVER_DECODE_ORDER");
+        return text && strtoul(text, nullptr, 10) == 0 ? 0u : 1u;
     }();
     return value;
 }
@@ -145,7 +145,7 @@ uint64_t workspace_bytes(const lk_decode_shape& s) {
 template <int QF>
 void launch_decode(const DecodeArgs& a, const Geometry& g, int kv, void* out, hipStream_t stream) {
     if (g.fast) {
-        const uint64_t grid = uint64_t(a.batch) * a.kv_heads * g.splits;
+        const uint64_t grid = uint64_t(a.batch) * g.splits * a.kv_heads;
         require(grid <= 0x7FFFFFFFull, "decode grid too large");
         if (kv == LK_BF16)
             hipLaunchKernelGGL((decode_split_mfma<LK_BF16, QF>), dim3(uint32_t(grid)), dim3(kWave * kDecodeWaves), 0, stream, a);
@@ -288,7 +288,7 @@ LK_EXPORT int lk_paged_decode(const lk_decode_shape* shape, const void* q, const
         a.groups = s.query_heads / s.kv_heads;
         a.splits = g.splits;
         a.bps = g.bps;
-        a.heads_inner = lk::env_heads_inner();
+        a.order = lk::env_order();
         a.block_bytes = lk::pool_block_bytes(s);
         a.scale_log2 = s.scale * lk::kLog2e;
         lk::require(lk::aligned(pool, s.kv_format == LK_F32 ? 4 : (s.kv_format == LK_BF16 ? 2 : 1)), "misaligned pool");
