@@ -188,3 +188,46 @@ def test_bf16_swap_round_trip_through_the_backend():
         assert np.array_equal(after, reference)
     finally:
         backend.close()
+
+
+@pytest.mark.parametrize("fp8", [True, False], ids=["fp8", "bf16"])
+def test_cpu_tier_offload_and_prefix_restore_on_the_gpu(fp8):
+    """CpuTier over the HIP backend (reference tier.py:41-186): the table's blocks stay held
+    until the copy completes, and a restored prefix equals the oracle's round trip."""
+    from layover_amd.kernels.fp8 import Fp8Layout
+    from layover_amd.kv.paged_cache import BlockTable
+    from layover_amd.kv.tier import CpuTier
+    from layover_amd.kv.transfer import NativeBackend
+
+    cache, bits = qwen_cache(16, seed=7 + fp8)
+    layout = Fp8Layout.from_cache(cache)
+    backend = NativeBackend("cuda", staging_bytes=3 * cache.block_bytes, ids_capacity=64)
+    tier = CpuTier(capacity_blocks=12, backend=backend, fp8=fp8)
+    try:
+        tier.prepare(cache)
+        table = BlockTable(cache.allocator.alloc(6), 6 * 16 - 5)
+        ids = list(table.blocks)
+        handle = tier.start_offload(cache, table)
+        assert table.blocks == [] and tier.used_blocks == 6
+        tier.wait_for(handle)
+        assert cache.allocator.num_used == 0 and not handle.in_flight
+        if fp8:
+            expected = oracle.quantize_records(bits, ids, layout.group_elems, layout.groups_per_block)
+        else:
+            expected = oracle.gather(bits, cache.block_bytes, ids)
+        assert np.array_equal(handle.payload.memory.numpy()[: expected.size], expected)
+
+        cache.pool.zero_()
+        prefix, ticket = tier.start_restore(cache, handle, blocks=4)
+        ticket.wait()
+        tier.poll()
+        assert prefix.num_tokens == 64 and tier.used_blocks == 0
+        after = cache.pool.view(torch.int16).cpu().numpy().view(np.uint16)
+        reference = np.zeros_like(bits)
+        if fp8:
+            oracle.dequantize_records(expected, prefix.blocks, reference, layout.group_elems, layout.groups_per_block)
+        else:
+            oracle.scatter(reference, cache.block_bytes, prefix.blocks, expected)
+        assert np.array_equal(after, reference)
+    finally:
+        backend.close()
