@@ -7,9 +7,11 @@ the reference's integer codec (fp8.py:86-137), run as gfx950 HIP kernels
 (layover_amd/csrc/fp8_codec.h) through liblayover_kernels.so. Kernels are enqueued on the
 current torch stream and return immediately.
 
-There is no CPU implementation here: a pool that is not on a GPU is refused, and a missing
-kernel library raises. (The CPU restatement used to check these kernels is test
-infrastructure in oracle/.)
+There is no CPU implementation of the codec here: a pool that is not on a GPU is refused,
+and a missing kernel library raises. (The CPU restatement used to check these kernels is test
+infrastructure in oracle/.) group_shifts and round_trip_bound are plain torch on any device:
+they price a round trip's error, as the reference's swap measurement does when it verifies an
+FP8 swap (bench/kv_crossover.py:213-216).
 """
 
 from __future__ import annotations
@@ -127,3 +129,46 @@ def decode_bits_hip(codes: torch.Tensor, shift: int = 0) -> torch.Tensor:
     out = torch.empty(codes.shape[0], dtype=torch.uint16, device=codes.device)
     _lib.check(_lib.load().lk_fp8_decode(codes.data_ptr(), out.data_ptr(), codes.shape[0], shift, _lib.current_stream(codes.device)))
     return out
+
+
+def group_shifts(bits: torch.Tensor) -> torch.Tensor:
+    """Per-group shift of BF16 bit patterns shaped [..., group_elems] (fp8.py:86-92): the largest
+    raw exponent among finite values with a nonzero exponent field, minus 134; 0 without one."""
+    raw = (bits.view(torch.int16).to(torch.int32) >> 7) & 0xFF
+    raw = torch.where(raw == 0xFF, torch.zeros_like(raw), raw)
+    largest = raw.amax(dim=-1)
+    return torch.where(largest > 0, largest - 134, torch.zeros_like(largest))
+
+
+def round_trip_bound(bits: torch.Tensor, shifts: torch.Tensor | None = None) -> torch.Tensor:
+    """Largest absolute error an FP8 round trip may leave on each value, float64, for BF16 bit
+    patterns shaped [..., group_elems] (fp8.py:140-152).
+
+    A value whose exponent minus the shift is at least -6 lands on an E4M3 normal, whose 3
+    stored bits round to within 1/16 of the value; below that it lands on the subnormal grid of
+    spacing 2^(shift-9), so within half of it. Nothing is ever required below 2^-126, the
+    smallest BF16 normal, since decoding flushes there."""
+    shifts = group_shifts(bits) if shifts is None else shifts
+    shifts = shifts.to(torch.int32)[..., None]
+    wide = bits.view(torch.int16).to(torch.int32)
+    exponent = ((wide >> 7) & 0xFF) - 127
+    magnitude = bits.view(torch.bfloat16).to(torch.float64).abs()
+    absolute = torch.pow(2.0, (shifts - 10).to(torch.float64)).expand_as(magnitude)
+    bound = torch.where(exponent - shifts >= -6, magnitude / 16, absolute)
+    return bound.clamp_min(2.0**-126)
+
+
+def round_trip_within_bound(before: torch.Tensor, after: torch.Tensor, group_elems: int, ignore_nonfinite: bool = False,
+                            slice_blocks: int = 16) -> bool:
+    """Whether BF16 blocks [block, ...] came back from an FP8 round trip within round_trip_bound
+    (fp8.py:155-176). Works a few blocks at a time, on whatever device the tensors are on;
+    groups never span blocks, so slicing leaves every shift unchanged. ignore_nonfinite skips
+    values that were infinite or NaN before the trip."""
+    for start in range(0, before.shape[0], slice_blocks):
+        bits = before[start : start + slice_blocks].contiguous().view(torch.uint16).reshape(-1, group_elems)
+        values = bits.view(torch.bfloat16).to(torch.float64)
+        gap = (after[start : start + slice_blocks].to(torch.float64).reshape(-1, group_elems) - values).abs()
+        within = gap <= round_trip_bound(bits)
+        if not bool((within[values.isfinite()] if ignore_nonfinite else within).all()):
+            return False
+    return True
