@@ -33,6 +33,12 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+# Measured HBM bytes per quantize launch over its algorithmic bytes (read + write), from two
+# rocprofv3 --pmc passes over this script (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch).
+# FETCH_SIZE counts half the bytes read by these kernels: lk_stream_probe's 8 GiB read shows
+# as 4 GiB, and its 4 GiB copy as 4 GiB of WRITE_SIZE. Per full 113-record launch:
+# 2 x 130,221 + 130,686 KiB measured against 390,636 KiB algorithmic.
+QUANTIZE_TRAFFIC_RATIO = 1.0012
 L4_FP8_SWAP_MS = 67.0  # README.md:27, :115 of the reference (NVIDIA L4)
 QWEN = dict(layers=36, kv_heads=8, query_heads=32, slots=16, head_dim=128)
 POOL_BYTES = 12 << 30
@@ -573,7 +579,9 @@ def main() -> None:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(q["achieved_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": round(q["bytes_per_launch"] * QUANTIZE_TRAFFIC_RATIO),
+            "traffic_source": "rocprofv3 --pmc FETCH_SIZE (x2) and WRITE_SIZE (x1) per dispatch of this command, "
+                              f"{QUANTIZE_TRAFFIC_RATIO} x algorithmic bytes; profiles/quantize_dequantize_fp8_swap_qwen3_4b.md",
             "bytes_per_launch": q["bytes_per_launch"],
             "mean_launch_us": round(q["mean_ms"] * 1e3, 2),
             "launches": q["launches"],

@@ -9,23 +9,22 @@
 // triton_decode.py:97-109). Scores are kept in base 2 (scale * log2 e folded into one
 // multiply) so the exponentials are single v_exp_f32 instructions.
 //
-// Fast path (16 slots x 128 dims, the Qwen3 shape; G = 1, 2, 4 or 8 query heads per KV head):
-//   workgroup = (sequence, KV head, split of `bps` blocks), 4 waves taking the split's blocks
-//   round-robin. Each K or V tile of a block (16 x 128) is read once for all G query heads:
-//   no GQA re-reads, so HBM traffic is the "unique" bytes of bench/decode_bandwidth.py:
-//   129-139. Lane l of a wave owns slots l/8 and l/8 + 8 and 16 of the 128 dims (c = l % 8):
-//   for BF16, dims c*8..c*8+7 and 64+c*8..64+c*8+7, which makes each 16-byte load
-//   instruction of the wave cover 8 whole 128-byte lines; for FP8, dims c*16..c*16+15.
-//   A score is a dot product over the lane's 16 dims (v_dot2_f32_bf16 for BF16 q and K)
-//   reduced over the 8 lanes of its slot with three DPP adds. Each lane keeps its own
-//   online-softmax state per head (m, l, 16 accumulators) over the slots it sees, so no
-//   per-tile cross-lane max is needed; the states of the 64 lanes and 4 waves are merged
-//   once at the end of the split. The running max is only raised (with a rescale of the
-//   accumulators) when a score exceeds it by more than 2^8, a wave-uniform branch that is
-//   almost never taken after the first tile; weights are then at most 2^8, harmless in FP32.
-//   FP8 tiles are dequantized in registers: codes -> FP32 by the hardware convert (exact),
-//   the group's power of two folded into the score (K) and the weights (V). Groups whose
-//   shift could leave BF16's normal range use the exact integer decode of fp8.py instead.
+// Fast path (16 slots x 128 dims, the Qwen3 shape; up to 16 query heads per KV head), on the
+//   matrix cores (details above decode_split_mfma): workgroup = (sequence, split of `bps`
+//   blocks, KV head), 4 waves taking the split's blocks round-robin, one (block, KV head) unit
+//   at a time. Each K or V tile (16 x 128) is read once for all G query heads: no GQA
+//   re-reads, so HBM traffic is the "unique" bytes of bench/decode_bandwidth.py:129-139.
+//   QK^T is four v_mfma_f32_16x16x32_bf16 (slots x heads); the online softmax runs per lane
+//   on the MFMA result (head n, four slots); PV is v_mfma_f32_16x16x16_bf16 with the weights
+//   as BF16 hi + lo parts, so they keep FP32-like precision. The running max is only raised
+//   (with a rescale of the accumulators) when a score exceeds it by more than 2^8, a
+//   wave-uniform branch almost never taken after the first tile; weights are then at most
+//   2^8, harmless in FP32. Tiles stream through a ring of register buffers refilled as they
+//   are consumed; block ids (and FP8 shifts) are loaded one per lane up front and read with
+//   v_readlane. FP8 tiles are dequantized in registers: codes -> BF16 by the hardware
+//   convert (exact), the group's power of two folded into the score (K) and the weights (V).
+//   Groups whose shift could leave BF16's normal range use the exact integer decode of
+//   fp8.py instead, so results equal attention over the reference's decode_bits output.
 // Generic path (any slots <= 64 and head_dim <= 256, any G): one wave per (sequence, query
 //   head, split), lane d owning dims d, d+64, ...; used for shapes other than Qwen3's.
 // Combine: one wave per (sequence, query head) merges the split partials (m, l, acc) and

@@ -5,7 +5,9 @@
 // 86-137), so every byte and every restored BF16 pattern is identical to its output by
 // construction, including the cases a hardware float convert treats differently (BF16
 // subnormals -> signed zero, infinity and overflow -> sign|0x7F, decode saturating at
-// 0x7F7F and flushing below BF16's smallest normal).
+// 0x7F7F and flushing below BF16's smallest normal). The Qwen3-shaped kernels of
+// fp8_records.hip use the hardware E4M3 converts instead, only for groups where those are
+// proven to give the same bytes, and this integer codec for every other group.
 //
 // Layout of work: one wave64 per group. A Qwen3-4B group (16 slots x 128 dims = 2048 values,
 // 4 KiB of BF16) is 4 loads of 16 bytes per lane, each wave instruction reading 1 KiB
