@@ -13,8 +13,14 @@ Also measured in the same run (extra keys of the JSON line):
   decode      BASELINE configs[2]: paged decode, batch 32, contexts U[1024, 32768], 36
               layers timed per layer, "unique" KV bytes (decode_bandwidth.py:129-139)
   decode_fp8  configs[3]: the same reading FP8 records, plus batch 1 @ 32,768 and 64 @ 4,096
+  decode_graphs  small-batch decode steps (token write + attention, 36 layers) replayed as
+              one HIP graph, against the same step launched eagerly; BF16 and FP8 pools
+  overlap     configs[4]: decode steps while 2,048 blocks swap out and back in
+  decode_distinct  configs[2] on a ~78 GB pool whose rows share no block
+  hbm_probe   lk_stream_probe read and copy rates: the measured HBM ceiling
   cpu_baseline  the oracle's C restatement of the FP8 swap arithmetic on a bounded sample,
               single-threaded on the host cores
+  cpu_reference_config1  configs[0] on the reference's own host library (oracle/_ref)
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-decode] [--skip-cpu]
 """
@@ -314,6 +320,57 @@ def decode_step_events(device, pool, table, lens, q, out, workspace, groups):
     return start, end
 
 
+def graph_decode_bench(device, cache, fp8_pool, steps: int = 20) -> list:
+    """Small-batch decode steps (every layer: write the new token, then paged attention) as
+    one HIP graph replay against the same step launched eagerly from Python, on the BF16 pool
+    and on the FP8-record pool. Rows use distinct random blocks of the 12 GiB pool."""
+    import numpy as np
+    import torch
+
+    from layover_amd.kv.decode_graphs import DecodeAttentionGraphs
+    from layover_amd.kv.paged_cache import BlockTable
+
+    runs = []
+    for kind, pool in (("bf16", None), ("fp8", fp8_pool)):
+        graphs = DecodeAttentionGraphs(cache, QWEN["query_heads"], pool=pool, sizes=(1, 8), max_tokens=32768)
+        rng = np.random.default_rng(11)
+        free = [b for b in rng.permutation(cache.allocator.num_blocks).tolist() if b != graphs.scratch]
+        for batch, tokens in ((1, 32768), (8, 4096)):
+            need = -(-tokens // 16)
+            tables = [BlockTable(free[i * need : (i + 1) * need], tokens) for i in range(batch)]
+            q = torch.randn(QWEN["layers"], batch, QWEN["query_heads"], QWEN["head_dim"], device=device).to(torch.bfloat16)
+            k = torch.randn(QWEN["layers"], batch, QWEN["kv_heads"], QWEN["head_dim"], device=device).to(torch.bfloat16)
+            graphs.run(tables, q, k, k.clone())
+            size = graphs.size_for(batch)
+            timings = {}
+            for mode, fn in (("graph", lambda: graphs.replay(size)), ("eager", lambda: graphs.step_eager(size))):
+                for _ in range(3):
+                    fn()
+                torch.cuda.synchronize()
+                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                start.record()
+                for _ in range(steps):
+                    fn()
+                end.record()
+                end.synchronize()
+                timings[mode] = start.elapsed_time(end) / steps
+            tile = QWEN["slots"] * QWEN["head_dim"]
+            per_block = QWEN["kv_heads"] * 2 * ((tile + 2) if kind == "fp8" else tile * 2)
+            kv_bytes = batch * need * per_block
+            runs.append({
+                "case": f"{kind}_batch{batch}_{tokens}",
+                "graph_per_layer_us": round(timings["graph"] * 1e3 / QWEN["layers"], 2),
+                "eager_per_layer_us": round(timings["eager"] * 1e3 / QWEN["layers"], 2),
+                "graph_kv_gbs": round(kv_bytes / (timings["graph"] * 1e-3 / QWEN["layers"]) / 1e9, 1),
+                "captured_size": size,
+            })
+        cache.allocator.decref(graphs.scratch)
+        del graphs
+        torch.cuda.empty_cache()
+    return runs
+
+
+
 def overlap_bench(device, cache, pool_blocks: int, swap_blocks: int = 2048) -> dict:
     """decode steps (batch 32, mixed contexts, BF16) on torch's stream
     while an FP8 swap of 2,048 blocks (32,768 tokens) runs on the backend's streams, then the
@@ -609,6 +666,8 @@ def main() -> None:
             run = decode_bench(device, cache.pool, lengths, args.decode_steps, 1, seed=4, kv_pool=fp8_pool)
             fp8_runs.append({"case": name, **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in run.items()}})
         result["decode_fp8"] = fp8_runs
+        log("decode steps as HIP graph replays (batch 1 and 8)")
+        result["decode_graphs"] = graph_decode_bench(device, cache, fp8_pool)
         del records, fp8_pool
         torch.cuda.empty_cache()
 

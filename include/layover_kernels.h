@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define LK_ABI_VERSION 1
+#define LK_ABI_VERSION 2
 
 enum { LK_OK = 0, LK_ERR_INVALID = 1, LK_ERR_DEVICE = 2 };
 
@@ -76,20 +76,38 @@ typedef struct {
     int32_t q_format;     /* LK_BF16 or LK_F32; out has the same format */
     int32_t kv_format;    /* LK_BF16, LK_F32 or LK_FP8_RECORD */
     float scale;          /* softmax scale, 1/sqrt(head_dim) in the reference */
+    uint32_t table_stride;   /* int32 elements between table rows; 0 means table_width */
+    uint32_t lengths_stride; /* int32 elements between lengths; 0 means 1 */
 } lk_decode_shape;
 
 /* Bytes of device workspace lk_paged_decode needs for this shape (split-K partial results).
- * Depends only on the shape, never on lengths, so it can be sized once per batch layout. */
+ * Depends only on the shape, never on lengths, so it can be sized once per batch layout. Its
+ * contents need no initialization. Calls that share a workspace must not overlap in time. */
 uint64_t lk_paged_decode_workspace(const lk_decode_shape* shape);
 
 /* One decode step of one layer: out[b, h] = softmax(q[b,h] . K^T * scale) V over the first
- * lengths[b] tokens of row b of `table` (int32 [batch, table_width]), where query head h
+ * lengths[b*lengths_stride] tokens of row b of `table` (int32, row b at b*table_stride, its
+ * first table_width entries used; the strides let the columns of a packed row block, as
+ * triton_decode.py takes them by stride, be passed without a copy), where query head h
  * reads KV head h / (query_heads / kv_heads). q and out are [batch, query_heads, head_dim]
  * contiguous. Tokens at or past lengths[b] never contribute, whatever their slots hold.
  * Accumulation is FP32; out is rounded to nearest even. Requires 1 <= lengths[b] <=
  * table_width*slots and every id in range, which the caller has checked. */
 int lk_paged_decode(const lk_decode_shape* shape, const void* q, const void* pool, const int32_t* table,
                     const int32_t* lengths, void* out, void* workspace, uint64_t workspace_bytes, void* stream);
+
+/* One decode step's KV write into an FP8-record pool: no reference counterpart (the
+ * reference writes BF16 tokens into a BF16 pool, layover/model.py:139-140). For row b,
+ * block write_block[b*row_stride] slot write_slot[b*row_stride] of layer `layer` takes
+ * k[b] (K) and v[b] (V), BF16 [batch, kv_heads, head_dim]. Each of the 2*kv_heads groups a
+ * row touches is re-encoded (as lk_fp8_quantize would encode it) from: the old codes decoded
+ * at the old shift for earlier slots, the new values at the write slot, and zero for later
+ * slots. Records are laid out as lk_fp8_quantize writes them, with group_elems =
+ * slots*head_dim and groups_per_block = 2*layers*kv_heads. Rows must name distinct blocks;
+ * ids and slots are not checked. */
+int lk_fp8_append(void* records, const int32_t* write_block, const int32_t* write_slot, uint32_t row_stride, uint32_t batch,
+                  const void* k, const void* v, uint32_t layer, uint32_t layers, uint32_t kv_heads, uint32_t slots,
+                  uint32_t head_dim, void* stream);
 
 /* Measurement support, no reference counterpart: stream `bytes` (a multiple of 16, 16-byte
  * aligned) from `src`, copying to `dst`, or only reading when dst is null (then `sink`, one

@@ -28,7 +28,9 @@
 // Generic path (any slots <= 64 and head_dim <= 256, any G): one wave per (sequence, query
 //   head, split), lane d owning dims d, d+64, ...; used for shapes other than Qwen3's.
 // Combine: one wave per (sequence, query head) merges the split partials (m, l, acc) and
-//   writes the output rounded to nearest even.
+//   writes the output rounded to nearest even. (Merging inside the split kernel, in the last
+//   split to finish, needs a device-scope release per workgroup; on MI355X that fence writes
+//   back the XCD's L2 and cost more than doubled the per-layer time at batch 32.)
 #ifndef LAYOVER_AMD_DECODE_ATTENTION_H
 #define LAYOVER_AMD_DECODE_ATTENTION_H
 
@@ -84,6 +86,8 @@ struct DecodeArgs {
     float* partial_acc;    // [batch, query_heads, splits, head_dim]
     float* partial_ml;     // [batch, query_heads, splits, 2]
     uint32_t batch, query_heads, kv_heads, head_dim, layers, slots, layer, table_width;
+    uint32_t table_stride;   // int32 elements from one table row to the next (>= table_width)
+    uint32_t lengths_stride; // int32 elements from one length to the next
     uint32_t groups;       // query heads per KV head
     uint32_t splits;       // splits per sequence (grid)
     uint32_t bps;          // blocks per split
@@ -206,7 +210,7 @@ __global__ __launch_bounds__(kWave* kDecodeWaves) void decode_split_mfma(DecodeA
     if (!decode_unit_of(a, blockIdx.x, &seq, &split, &kv_head)) return;
     const uint32_t groups = a.groups;
 
-    const int32_t length = a.lengths[seq];
+    const int32_t length = a.lengths[uint64_t(seq) * a.lengths_stride];
     const uint32_t nblocks = blocks_of(length, kSlots);
     const uint32_t first = split * a.bps;
     if (first >= nblocks) return;
@@ -250,7 +254,7 @@ __global__ __launch_bounds__(kWave* kDecodeWaves) void decode_split_mfma(DecodeA
     const uint64_t k_offset = head_tile * tile_bytes + (uint64_t(n) * kDim + 32 * g) * kElem;
     const uint64_t v_offset = (uint64_t(a.layers) * a.kv_heads + head_tile) * tile_bytes + (uint64_t(4 * g) * kDim + 8 * n) * kElem;
     const uint64_t block_elems = uint64_t(2) * a.layers * a.kv_heads * kSlots * kDim;  // FP8: shifts follow the data
-    const int32_t* row_ids = a.table + uint64_t(seq) * a.table_width + first;
+    const int32_t* row_ids = a.table + uint64_t(seq) * a.table_stride + first;
 
     // The block ids (and FP8 shifts) of this wave's units, one unit per lane (at most 64:
     // blocks per split <= 256), loaded before any tile and read back with v_readlane, so no
@@ -507,7 +511,7 @@ __global__ __launch_bounds__(kWave) void decode_split_generic(DecodeArgs a) {
     const uint32_t qh = pair % a.query_heads;
     const uint32_t seq = pair / a.query_heads;
     const uint32_t kv_head = qh / a.groups;
-    const int32_t length = a.lengths[seq];
+    const int32_t length = a.lengths[uint64_t(seq) * a.lengths_stride];
     const uint32_t nblocks = blocks_of(length, a.slots);
     const uint32_t first = split * a.bps;
     if (first >= nblocks) return;
@@ -534,7 +538,7 @@ __global__ __launch_bounds__(kWave) void decode_split_generic(DecodeArgs a) {
 
     float m = -INFINITY, l = 0.0f;
     for (uint32_t b = first; b < last; ++b) {
-        const uint8_t* base = a.pool + uint64_t(a.table[uint64_t(seq) * a.table_width + b]) * a.block_bytes;
+        const uint8_t* base = a.pool + uint64_t(a.table[uint64_t(seq) * a.table_stride + b]) * a.block_bytes;
         const uint8_t* k_tile = base + head_tile * tile_elems * kElem;
         const uint8_t* v_tile = base + v_group * tile_elems * kElem;
         int32_t ks = 0, vs = 0;
@@ -587,7 +591,7 @@ __global__ __launch_bounds__(kWave) void decode_combine(DecodeArgs a, void* out)
     const uint32_t lane = threadIdx.x;
     const uint32_t qh = blockIdx.x % a.query_heads;
     const uint32_t seq = blockIdx.x / a.query_heads;
-    const uint32_t used = (blocks_of(a.lengths[seq], a.slots) + a.bps - 1) / a.bps;
+    const uint32_t used = (blocks_of(a.lengths[uint64_t(seq) * a.lengths_stride], a.slots) + a.bps - 1) / a.bps;
     const uint64_t base = (uint64_t(seq) * a.query_heads + qh) * a.splits;
     const float* ml = a.partial_ml + 2 * base;
 

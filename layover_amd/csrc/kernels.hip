@@ -137,6 +137,7 @@ void check_shape(const lk_decode_shape& s) {
     require(s.slots <= 1024, "more than 1024 slots per block is not supported");
 }
 
+// Workspace: split partials, acc [batch, query_heads, splits, head_dim] then (m, l) pairs.
 uint64_t workspace_bytes(const lk_decode_shape& s) {
     const Geometry g = geometry(s);
     return uint64_t(s.batch) * s.query_heads * g.splits * (uint64_t(s.head_dim) + 2) * sizeof(float);
@@ -187,6 +188,124 @@ __global__ __launch_bounds__(256) void stream_probe(const u32x4* __restrict__ sr
         hash ^= w[0] ^ w[1] ^ w[2] ^ w[3];
     }
     if (hash == 0x9E3779B9u) *sink = hash;
+}
+
+
+// One token per sequence written into an FP8-record pool (lk_fp8_append). One wave per
+// (row, kind, KV head) group: element e of the group (slot e / head_dim) becomes the old
+// value decoded at the old shift for slots before the write slot, the new BF16 value at the
+// write slot, and zero after it; the group is then re-encoded at the shift of those values,
+// with the reference's integer codec (fp8.py:86-137). Each lane reads and writes only its
+// own elements, and the old shift is read before the wave max that precedes its overwrite.
+__global__ __launch_bounds__(kWave* kCodecWaves) void append_groups(uint8_t* __restrict__ records, const int32_t* __restrict__ write_block,
+                                                                  const int32_t* __restrict__ write_slot, uint32_t row_stride,
+                                                                  uint32_t batch, const uint16_t* __restrict__ k,
+                                                                  const uint16_t* __restrict__ v, uint32_t layer, uint32_t layers,
+                                                                  uint32_t kv_heads, uint32_t slots, uint32_t head_dim) {
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint64_t unit = uint64_t(blockIdx.x) * kCodecWaves + threadIdx.x / kWave;
+    if (unit >= uint64_t(batch) * 2 * kv_heads) return;
+    const uint32_t head = uint32_t(unit % kv_heads);
+    const uint32_t kind = uint32_t(unit / kv_heads % 2);
+    const uint32_t row = uint32_t(unit / (2ull * kv_heads));
+    const uint64_t group_elems = uint64_t(slots) * head_dim;
+    const uint32_t groups_per_block = 2 * layers * kv_heads;
+    const uint64_t block_elems = group_elems * groups_per_block;
+    const uint64_t record = block_elems + 2ull * groups_per_block;
+    const uint32_t g = (kind * layers + layer) * kv_heads + head;
+    uint8_t* base = records + uint64_t(uint32_t(write_block[uint64_t(row) * row_stride])) * record;
+    uint8_t* codes = base + uint64_t(g) * group_elems;
+    uint8_t* shift_at = base + block_elems + 2ull * g;
+    const uint32_t slot = uint32_t(write_slot[uint64_t(row) * row_stride]);
+    const uint16_t* fresh = (kind == 0 ? k : v) + (uint64_t(row) * kv_heads + head) * head_dim;
+    const int32_t old_shift = int16_t(uint16_t(shift_at[0]) | uint16_t(shift_at[1] << 8));
+
+    auto value = [&](uint64_t e) -> uint32_t {
+        const uint64_t s = e / head_dim;
+        if (s < slot) return decode_e4m3(codes[e], old_shift);
+        if (s == slot) return fresh[e - s * head_dim];
+        return 0u;
+    };
+    uint32_t key = 0;
+    for (uint64_t e = lane; e < group_elems; e += kWave) {
+        const uint32_t k_ = exponent_key(value(e));
+        key = k_ > key ? k_ : key;
+    }
+    const int32_t shift = shift_from_key(wave_max(key));
+    for (uint64_t e = lane; e < group_elems; e += kWave) codes[e] = uint8_t(encode_e4m3(value(e), shift));
+    if (lane == 0) {
+        const uint16_t stored = uint16_t(int16_t(shift));
+        shift_at[0] = uint8_t(stored & 0xFFu);
+        shift_at[1] = uint8_t(stored >> 8);
+    }
+}
+
+
+// The same for Qwen3-shaped groups (16 slots x 128 dims, 16-byte aligned records, k and v):
+// lane l holds bytes 32l .. 32l+31 of the group, i.e. slot l/4 and dims 32(l%4) .. +31, in
+// registers from two 16-byte loads, so the group is read once and written once.
+__global__ __launch_bounds__(kWave* kCodecWaves) void append_groups_2048(uint8_t* __restrict__ records, const int32_t* __restrict__ write_block,
+                                                                       const int32_t* __restrict__ write_slot, uint32_t row_stride,
+                                                                       uint32_t batch, const uint16_t* __restrict__ k,
+                                                                       const uint16_t* __restrict__ v, uint32_t layer, uint32_t layers,
+                                                                       uint32_t kv_heads) {
+    constexpr uint32_t kDims = 128;
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint64_t unit = uint64_t(blockIdx.x) * kCodecWaves + threadIdx.x / kWave;
+    if (unit >= uint64_t(batch) * 2 * kv_heads) return;
+    const uint32_t head = uint32_t(unit % kv_heads);
+    const uint32_t kind = uint32_t(unit / kv_heads % 2);
+    const uint32_t row = uint32_t(unit / (2ull * kv_heads));
+    const uint32_t groups_per_block = 2 * layers * kv_heads;
+    const uint64_t block_elems = uint64_t(kFastGroup) * groups_per_block;
+    const uint64_t record = block_elems + 2ull * groups_per_block;
+    const uint32_t g = (kind * layers + layer) * kv_heads + head;
+    uint8_t* base = records + uint64_t(uint32_t(write_block[uint64_t(row) * row_stride])) * record;
+    u32x4* codes = reinterpret_cast<u32x4*>(base + uint64_t(g) * kFastGroup) + 2 * lane;
+    int16_t* shift_at = reinterpret_cast<int16_t*>(base + block_elems + 2ull * g);
+    const uint32_t write = uint32_t(write_slot[uint64_t(row) * row_stride]);
+    const uint32_t slot = lane / 4;
+    const int32_t old_shift = *shift_at;
+
+    const u32x4 old[2] = {codes[0], codes[1]};
+    uint32_t pairs[16];  // the lane's 32 new BF16 values, two per word
+    if (slot < write) {
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+            const uint32_t word = old[w / 4][w % 4];
+            pairs[2 * w] = decode_e4m3(word & 0xFFu, old_shift) | (decode_e4m3((word >> 8) & 0xFFu, old_shift) << 16);
+            pairs[2 * w + 1] = decode_e4m3((word >> 16) & 0xFFu, old_shift) | (decode_e4m3(word >> 24, old_shift) << 16);
+        }
+    } else if (slot == write) {
+        const u32x4* fresh = reinterpret_cast<const u32x4*>((kind == 0 ? k : v) + (uint64_t(row) * kv_heads + head) * kDims + 32 * (lane % 4));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const u32x4 w = fresh[j];
+#pragma unroll
+            for (int x = 0; x < 4; ++x) pairs[4 * j + x] = w[x];
+        }
+    } else {
+#pragma unroll
+        for (int x = 0; x < 16; ++x) pairs[x] = 0u;
+    }
+    uint32_t key = 0;
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+        const uint32_t lo = exponent_key(pairs[x] & 0xFFFFu), hi = exponent_key(pairs[x] >> 16);
+        key = lo > key ? lo : key;
+        key = hi > key ? hi : key;
+    }
+    const int32_t shift = shift_from_key(wave_max(key));
+    u32x4 out[2];
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+        const uint32_t a = pairs[2 * w], b = pairs[2 * w + 1];
+        out[w / 4][w % 4] = encode_e4m3(a & 0xFFFFu, shift) | (encode_e4m3(a >> 16, shift) << 8) | (encode_e4m3(b & 0xFFFFu, shift) << 16) |
+                            (encode_e4m3(b >> 16, shift) << 24);
+    }
+    codes[0] = out[0];
+    codes[1] = out[1];
+    if (lane == 0) *shift_at = int16_t(shift);
 }
 
 }  // namespace lk
@@ -250,6 +369,31 @@ LK_EXPORT int lk_fp8_decode(const uint8_t* codes, uint16_t* out, uint64_t n, int
     });
 }
 
+LK_EXPORT int lk_fp8_append(void* records, const int32_t* write_block, const int32_t* write_slot, uint32_t row_stride,
+                            uint32_t batch, const void* k, const void* v, uint32_t layer, uint32_t layers, uint32_t kv_heads,
+                            uint32_t slots, uint32_t head_dim, void* stream) {
+    return lk::guarded([&] {
+        lk::require(records && write_block && write_slot && k && v, "null records, write rows, k or v");
+        lk::require(layers > 0 && kv_heads > 0 && slots > 0 && head_dim > 0, "every record dimension must be positive");
+        lk::require(layer < layers, "layer out of range");
+        lk::require(row_stride > 0, "row_stride must be positive");
+        if (batch == 0) return;
+        const uint64_t waves = uint64_t(batch) * 2 * kv_heads;
+        const uint32_t grid = lk::grid_for_groups(waves);
+        const uint64_t record = uint64_t(slots) * head_dim * 2 * layers * kv_heads + 4ull * layers * kv_heads;
+        if (slots * head_dim == lk::kFastGroup && head_dim == 128 && record % 16 == 0 && lk::aligned(records, 16) && lk::aligned(k, 16) &&
+            lk::aligned(v, 16)) {
+            hipLaunchKernelGGL(lk::append_groups_2048, dim3(grid), dim3(lk::kWave * lk::kCodecWaves), 0, static_cast<hipStream_t>(stream),
+                               static_cast<uint8_t*>(records), write_block, write_slot, row_stride, batch, static_cast<const uint16_t*>(k),
+                               static_cast<const uint16_t*>(v), layer, layers, kv_heads);
+            return;
+        }
+        hipLaunchKernelGGL(lk::append_groups, dim3(grid), dim3(lk::kWave * lk::kCodecWaves), 0, static_cast<hipStream_t>(stream),
+                           static_cast<uint8_t*>(records), write_block, write_slot, row_stride, batch, static_cast<const uint16_t*>(k),
+                           static_cast<const uint16_t*>(v), layer, layers, kv_heads, slots, head_dim);
+    });
+}
+
 LK_EXPORT uint64_t lk_paged_decode_workspace(const lk_decode_shape* shape) {
     if (shape == nullptr) return 0;
     try {
@@ -285,6 +429,9 @@ LK_EXPORT int lk_paged_decode(const lk_decode_shape* shape, const void* q, const
         a.slots = s.slots;
         a.layer = s.layer;
         a.table_width = s.table_width;
+        a.table_stride = s.table_stride != 0 ? s.table_stride : s.table_width;
+        a.lengths_stride = s.lengths_stride != 0 ? s.lengths_stride : 1;
+        lk::require(a.table_stride >= s.table_width, "table_stride is smaller than table_width");
         a.groups = s.query_heads / s.kv_heads;
         a.splits = g.splits;
         a.bps = g.bps;

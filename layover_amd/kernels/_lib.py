@@ -12,8 +12,9 @@ from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_uint32, c_uint6
 
 from layover_amd.kv.native import NativeUnavailable, build_dir, hip_runtimes_loaded
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 LK_BF16, LK_F32, LK_FP8_RECORD = 0, 1, 2
+LK_OK, LK_ERR_INVALID, LK_ERR_DEVICE = 0, 1, 2
 LIBRARY_NAME = "liblayover_kernels.so"
 
 
@@ -38,6 +39,8 @@ class DecodeShape(ctypes.Structure):
         ("q_format", c_int32),
         ("kv_format", c_int32),
         ("scale", c_float),
+        ("table_stride", c_uint32),
+        ("lengths_stride", c_uint32),
     ]
 
 
@@ -50,6 +53,8 @@ SIGNATURES = {
     "lk_paged_decode_workspace": (c_uint64, [POINTER(DecodeShape)]),
     "lk_paged_decode": (c_int, [POINTER(DecodeShape), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint64, c_void_p]),
     "lk_stream_probe": (c_int, [c_void_p, c_void_p, c_uint64, c_void_p, c_void_p]),
+    "lk_fp8_append": (c_int, [c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32,
+                              c_uint32, c_uint32, c_void_p]),
 }
 
 _lib: ctypes.CDLL | None = None

@@ -58,6 +58,41 @@ class Fp8KVPool:
     def is_contiguous(self) -> bool:
         return self.records.is_contiguous()
 
+    def write(self, write_blocks: torch.Tensor, write_slots: torch.Tensor, layer: int, k: torch.Tensor, v: torch.Tensor) -> None:
+        """Write one token per row into layer `layer`, the FP8 counterpart of the reference's
+        decode-time pool assignment (model.py:139-140): k and v are BF16 [batch, kv_heads,
+        head_dim]; row b goes to slot write_slots[b] of block write_blocks[b]. Each group it
+        touches is re-encoded at a new shift (a new value may raise the group's largest
+        exponent), from the old values decoded at the old shift for earlier slots, the new
+        value at the write slot, and zero for the later slots, which no length covers yet.
+        write_blocks and write_slots are int32 on the pool's device, 1-D with one stride
+        between rows (columns of PagedKVCache.decode_rows are accepted as they are). Ids are
+        not checked against the pool: the caller has (as decode_rows does). Rows must name
+        distinct (block, layer) groups; two rows writing one group race. Enqueued on the
+        current stream."""
+        if not 0 <= layer < self.layers:
+            raise ValueError(f"layer {layer} out of range for {self.layers} layers")
+        batch = write_blocks.shape[0]
+        for name, rows in (("write_blocks", write_blocks), ("write_slots", write_slots)):
+            if rows.dtype != torch.int32 or rows.dim() != 1 or rows.shape[0] != batch:
+                raise ValueError(f"{name} must be 1-D int32 with one entry per row")
+        if batch and write_blocks.stride(0) != write_slots.stride(0):
+            raise ValueError("write_blocks and write_slots must share one row stride")
+        expected = (batch, self.kv_heads, self.head_dim)
+        for name, t in (("k", k), ("v", v)):
+            if t.dtype != torch.bfloat16 or tuple(t.shape) != expected or not t.is_contiguous():
+                raise ValueError(f"{name} must be contiguous BF16 shaped {expected}")
+        devices = {self.records.device, write_blocks.device, write_slots.device, k.device, v.device}
+        if len(devices) != 1 or self.records.device.type != "cuda":
+            raise ValueError("the pool, rows, k and v must be on one GPU")
+        if batch == 0:
+            return
+        _lib.check(
+            _lib.load().lk_fp8_append(self.records.data_ptr(), write_blocks.data_ptr(), write_slots.data_ptr(), write_blocks.stride(0),
+                                      batch, k.data_ptr(), v.data_ptr(), layer, self.layers, self.kv_heads, self.slots,
+                                      self.head_dim, _lib.current_stream(self.records.device))
+        )
+
     @classmethod
     def empty(cls, blocks: int, layers: int, kv_heads: int, slots: int, head_dim: int, device) -> "Fp8KVPool":
         layout = Fp8Layout(slots * head_dim, KV_KINDS * layers * kv_heads)
@@ -121,12 +156,32 @@ def validate(q, pool, layer, block_table, lengths, kv_groups) -> None:
         raise ValueError(f"block ids in [{lowest}, {highest}] are outside a pool of {blocks} blocks")
 
 
-def decode_shape(q, pool, layer, block_table, kv_groups) -> _lib.DecodeShape:
+def decode_shape(q, pool, layer, block_table, kv_groups, lengths=None) -> _lib.DecodeShape:
+    """The launch's shape; the table's row stride and the lengths' stride are taken from the
+    tensors, so columns of a packed row block (PagedKVCache.decode_rows) pass without a copy,
+    as the reference's launcher passes strides (triton_decode.py:131-179)."""
     batch, query_heads, head_dim = q.shape
     _, _, layers, kv_heads, slots, _ = pool.shape
     kv_format = _lib.LK_FP8_RECORD if _is_fp8(pool) else _FORMATS[pool.dtype]
+    table_stride = block_table.stride(0) if block_table.dim() == 2 else block_table.shape[-1]
+    lengths_stride = lengths.stride(0) if lengths is not None and lengths.dim() == 1 else 1
     return _lib.DecodeShape(batch, query_heads, kv_heads, head_dim, layers, slots, layer, block_table.shape[1],
-                            _FORMATS[q.dtype], kv_format, 1.0 / math.sqrt(head_dim))
+                            _FORMATS[q.dtype], kv_format, 1.0 / math.sqrt(head_dim), table_stride, lengths_stride)
+
+
+def _check_layout(q, block_table, lengths, out) -> None:
+    """What the kernel assumes of memory layout, checked from tensor metadata alone (no device
+    reads): a wrong stride would make it read the wrong rows, or past the table."""
+    if not (q.is_contiguous() and out.is_contiguous() and out.shape == q.shape and out.dtype == q.dtype):
+        raise ValueError("q and out must be contiguous tensors of one shape and dtype")
+    if block_table.dtype != torch.int32 or lengths.dtype != torch.int32:
+        raise ValueError("the block table and lengths must be int32 for the kernel")
+    if block_table.dim() != 2 or lengths.dim() != 1 or not lengths.shape[0] == block_table.shape[0] == q.shape[0]:
+        raise ValueError("the block table must be [batch, width] and lengths [batch]")
+    if block_table.shape[1] > 1 and block_table.stride(1) != 1:
+        raise ValueError("block table rows must be contiguous (any row stride)")
+    if block_table.stride(0) < block_table.shape[1] or lengths.stride(0) < 1:
+        raise ValueError("the block table's rows must not overlap")
 
 
 def workspace_bytes(shape: _lib.DecodeShape) -> int:
@@ -134,10 +189,12 @@ def workspace_bytes(shape: _lib.DecodeShape) -> int:
 
 
 def run_kernel(q, pool, layer, block_table, lengths, kv_groups, out, workspace=None) -> None:
-    """Launch without validating, on the current stream. q, table, lengths and out must be
-    contiguous, table and lengths int32."""
+    """Launch without validating values, on the current stream. q and out contiguous; table
+    int32 [batch, width] with contiguous rows at any row stride; lengths int32 [batch] at any
+    stride. A workspace passed in must not be in use by another launch at the same time."""
+    _check_layout(q, block_table, lengths, out)
     lib = _lib.load()
-    shape = decode_shape(q, pool, layer, block_table, kv_groups)
+    shape = decode_shape(q, pool, layer, block_table, kv_groups, lengths)
     need = int(lib.lk_paged_decode_workspace(shape))
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=q.device)

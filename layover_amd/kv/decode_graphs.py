@@ -1,0 +1,149 @@
+"""HIP graphs for the decode data path at small batch sizes.
+
+Mirrors the reference's layover/decode_graphs.py:1-100 on this path. At batch 1 the GPU's
+attention work per layer is tens of microseconds, so issuing each layer's launches from
+Python sets the pace; a graph records a step's launches once and replays them as one. The
+reference captures its whole model step; the model is outside this package, so the unit
+captured here is the data path's share of a step: for every layer, the new token's K/V write
+into the pool (model.py:139-140, or Fp8KVPool.write for an FP8-resident pool) and paged decode
+attention over the block table.
+
+As in the reference, each captured batch size gets fixed input tensors: one packed int32
+block of rows (write block, write slot, length, block table of fixed width, as
+PagedKVCache.decode_rows builds them), q for every layer, and the new tokens' K and V. A
+batch smaller than a captured size is padded with rows of length 1 that write and read slot 0
+of a scratch block reserved here and never handed out, so a padded row cannot touch a real
+sequence's KV. Larger batches, or tables wider than the captured width, get None and run
+eagerly. The decode workspace of each size is allocated once, before capture. Padding rows all
+write the scratch block's slot 0; what it holds is never read by a real row.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Callable
+
+import torch
+
+from layover_amd.kernels import hip_decode
+from layover_amd.kernels.hip_decode import Fp8KVPool
+from layover_amd.kv.paged_cache import BlockTable, PagedKVCache
+
+DEFAULT_SIZES = (1, 2, 4, 8)
+
+
+def hip_graph(step: Callable[[], torch.Tensor], pool=None) -> tuple[Callable[[], None], torch.Tensor, object]:
+    """Capture `step` after running it twice on a side stream (torch's graph capture rules);
+    returns a replay function, the output tensor each replay refreshes, and the graph's memory
+    pool for the next capture to share (reference decode_graphs.py:28-40)."""
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, pool=pool):
+        out = step()
+    return graph.replay, out, graph.pool()
+
+
+def eager_graph(step: Callable[[], torch.Tensor], pool=None) -> tuple[Callable[[], None], torch.Tensor, object]:
+    """Runs `step` on every replay instead: the same buffers without a capture (reference
+    decode_graphs.py:43-46)."""
+    out = step()
+    return (lambda: out.copy_(step())), out, pool
+
+
+class DecodeAttentionGraphs:
+    def __init__(self, cache: PagedKVCache, query_heads: int, pool: torch.Tensor | Fp8KVPool | None = None,
+                 sizes: tuple[int, ...] = DEFAULT_SIZES, max_tokens: int | None = None, capture: Callable = hip_graph,
+                 q_dtype: torch.dtype = torch.bfloat16):
+        """cache supplies the block allocator (for the scratch block) and the shape; `pool`
+        is what the steps write and read: the cache's BF16 pool by default, or an Fp8KVPool
+        of the same number of blocks."""
+        self.cache = cache
+        self.pool = cache.pool if pool is None else pool
+        cfg = cache.cfg
+        self.layers, self.kv_heads, self.head_dim = cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim
+        if query_heads % self.kv_heads:
+            raise ValueError(f"{query_heads} query heads do not divide into {self.kv_heads} KV heads")
+        self.query_heads = query_heads
+        self.groups = query_heads // self.kv_heads
+        self.sizes = tuple(sorted(sizes))
+        max_tokens = max_tokens or cache.allocator.num_blocks * cache.block_tokens
+        self.width = min(cache.blocks_for(max_tokens), cache.allocator.num_blocks)
+        self.scratch = cache.allocator.alloc(1)[0]
+        device = cache.device
+        largest = self.sizes[-1]
+        self.packed = torch.zeros(largest, 3 + self.width, dtype=torch.int32, device=device)
+        self.packed.copy_(self._padding(largest))
+        self.q = torch.zeros(self.layers, largest, query_heads, self.head_dim, dtype=q_dtype, device=device)
+        kv_dtype = torch.bfloat16 if isinstance(self.pool, Fp8KVPool) else self.pool.dtype
+        self.k_new = torch.zeros(self.layers, largest, self.kv_heads, self.head_dim, dtype=kv_dtype, device=device)
+        self.v_new = torch.zeros_like(self.k_new)
+        self._workspaces = {}
+        for size in self.sizes:
+            shape = hip_decode.decode_shape(self.q[0, :size], self.pool, 0, self.packed[:size, 3:], self.groups)
+            self._workspaces[size] = torch.empty(max(hip_decode.workspace_bytes(shape), 4), dtype=torch.uint8, device=device)
+        self._replays: dict[int, tuple[Callable[[], None], torch.Tensor]] = {}
+        graph_pool = None
+        for size in reversed(self.sizes):  # largest first, so the smaller ones fit in its pool
+            replay, out, graph_pool = capture(lambda size=size: self._step(size), graph_pool)
+            self._replays[size] = (replay, out)
+
+    def _padding(self, rows: int) -> torch.Tensor:
+        """Rows of length 1 that write and read slot 0 of the scratch block."""
+        row = torch.zeros(3 + self.width, dtype=torch.int32)
+        row[0], row[1], row[2], row[3] = self.scratch, 0, 1, self.scratch
+        return row.repeat(rows, 1)
+
+    def _step(self, size: int) -> torch.Tensor:
+        packed = self.packed[:size]
+        table, lengths = packed[:, 3:], packed[:, 2]
+        blocks, slots = packed[:, 0], packed[:, 1]
+        out = torch.empty(self.layers, size, self.query_heads, self.head_dim, dtype=self.q.dtype, device=self.q.device)
+        workspace = self._workspaces[size]
+        for layer in range(self.layers):
+            if isinstance(self.pool, Fp8KVPool):
+                self.pool.write(blocks, slots, layer, self.k_new[layer, :size], self.v_new[layer, :size])
+            else:
+                self.pool[blocks.long(), 0, layer, :, slots.long()] = self.k_new[layer, :size]
+                self.pool[blocks.long(), 1, layer, :, slots.long()] = self.v_new[layer, :size]
+            hip_decode.run_kernel(self.q[layer, :size], self.pool, layer, table, lengths, self.groups, out[layer], workspace)
+        return out
+
+    def replay(self, size: int) -> torch.Tensor:
+        """Replay the captured step of `size` rows on the buffers as they stand; returns the
+        output tensor that every replay of this size refreshes."""
+        replay, out = self._replays[size]
+        replay()
+        return out
+
+    def step_eager(self, size: int) -> torch.Tensor:
+        """The same step launched eagerly on the same buffers, for comparison."""
+        return self._step(size)
+
+    def size_for(self, batch: int) -> int | None:
+        return next((size for size in self.sizes if size >= batch), None)
+
+    def run(self, tables: list[BlockTable], q: torch.Tensor, k_new: torch.Tensor, v_new: torch.Tensor) -> torch.Tensor | None:
+        """Attention outputs [layers, batch, query_heads, head_dim] for one decode step of
+        tables already prepared for writing (each num_tokens counts the new token), or None
+        when no graph fits. q is [layers, batch, query_heads, head_dim]; k_new and v_new are
+        [layers, batch, kv_heads, head_dim]. Rows are checked on the host by decode_rows, as
+        an eager step's are (reference decode_graphs.py:88-100)."""
+        size = self.size_for(len(tables))
+        if size is None or max(len(t.blocks) for t in tables) > self.width:
+            return None
+        batch = len(tables)
+        rows = torch.cat([self.cache.decode_rows(tables, self.width), self._padding(size - batch)])
+        self.packed[:size].copy_(rows.to(self.packed.device), non_blocking=True)
+        self.q[:, :batch].copy_(q)
+        self.q[:, batch:size].zero_()
+        self.k_new[:, :batch].copy_(k_new)
+        self.v_new[:, :batch].copy_(v_new)
+        self.k_new[:, batch:size].zero_()
+        self.v_new[:, batch:size].zero_()
+        out = self.replay(size)
+        # The graph refreshes the same tensor on its next replay.
+        return out[:, :batch].clone()

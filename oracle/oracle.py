@@ -121,6 +121,32 @@ def scatter(pool: np.ndarray, block_bytes: int, ids, data: np.ndarray) -> None:
     lib().oracle_scatter(pool.ctypes.data, block_bytes, _ptr(ids), len(ids), _ptr(data))
 
 
+def append_tokens(records: np.ndarray, layers: int, kv_heads: int, slots: int, head_dim: int, write_blocks, write_slots,
+                  layer: int, k_bits: np.ndarray, v_bits: np.ndarray) -> np.ndarray:
+    """The FP8-resident pool's decode-time write (no reference counterpart; its BF16 analogue
+    is the pool assignment of model.py:139-140), composed only of dequantize_records and
+    quantize_records above: the block is dequantized, each touched group gets the new token at
+    its write slot and zero after it, the block is quantized again, and only the touched
+    groups' codes and shifts are copied back. records uint8 [blocks, record_bytes]; k_bits and
+    v_bits uint16 [rows, kv_heads, head_dim]. Returns new records."""
+    group_elems, groups_per_block = slots * head_dim, 2 * layers * kv_heads
+    block_elems = group_elems * groups_per_block
+    out = np.array(records, dtype=np.uint8, copy=True)
+    for row, (block, slot) in enumerate(zip(np.asarray(write_blocks).tolist(), np.asarray(write_slots).tolist())):
+        bits = np.zeros((1, 2, layers, kv_heads, slots, head_dim), dtype=np.uint16)
+        dequantize_records(out[block], [0], bits, group_elems, groups_per_block)
+        for kind, fresh in ((0, k_bits), (1, v_bits)):
+            bits[0, kind, layer, :, slot, :] = fresh[row]
+            bits[0, kind, layer, :, slot + 1 :, :] = 0
+        again = quantize_records(bits, [0], group_elems, groups_per_block)
+        for kind in (0, 1):
+            for head in range(kv_heads):
+                g = (kind * layers + layer) * kv_heads + head
+                out[block, g * group_elems : (g + 1) * group_elems] = again[g * group_elems : (g + 1) * group_elems]
+                out[block, block_elems + 2 * g : block_elems + 2 * g + 2] = again[block_elems + 2 * g : block_elems + 2 * g + 2]
+    return out
+
+
 def decode_attention(q: np.ndarray, pool_bits: np.ndarray, layer: int, table: np.ndarray, lengths: np.ndarray,
                      kv_groups: int, scale: float | None = None) -> np.ndarray:
     """decode_attention.py:9-37 in float64. q [batch, query_heads, dim] (any float dtype, or

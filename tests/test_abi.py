@@ -1,6 +1,7 @@
 """The C-ABI libraries load without a GPU and export exactly what include/*.h declares.
 No compute calls: on a machine without a GPU only loading and symbol lookup are checked."""
 
+import ctypes
 import re
 import subprocess
 from pathlib import Path
@@ -44,7 +45,7 @@ def test_kernel_library_exports_every_declared_symbol():
     assert path.exists(), f"{path} is not built"
     names = declared("layover_kernels.h")
     assert names == {"lk_abi_version", "lk_last_error", "lk_fp8_quantize", "lk_fp8_dequantize", "lk_fp8_encode",
-                     "lk_fp8_decode", "lk_paged_decode_workspace", "lk_paged_decode", "lk_stream_probe"}
+                     "lk_fp8_decode", "lk_paged_decode_workspace", "lk_paged_decode", "lk_stream_probe", "lk_fp8_append"}
     assert names <= exported(path)
     assert set(_lib.SIGNATURES) | {"lk_abi_version", "lk_last_error"} == names
 
@@ -53,7 +54,7 @@ def test_hip_libraries_load_into_one_hip_runtime_without_a_gpu():
     lib = native.load_library("hip")
     assert lib.lt_abi_version() == 2 and lib.lt_flavor() == b"hip"
     kernels = _lib.load()
-    assert kernels.lk_abi_version() == 1
+    assert kernels.lk_abi_version() == 2
     assert len(native.hip_runtimes_loaded()) == 1
 
 
@@ -61,6 +62,20 @@ def test_decode_workspace_depends_on_shape_only_and_refuses_nonsense():
     kernels = _lib.load()
     shape = _lib.DecodeShape(32, 32, 8, 128, 36, 16, 0, 2048, _lib.LK_BF16, _lib.LK_BF16, 128**-0.5)
     size = kernels.lk_paged_decode_workspace(shape)
-    assert size > 0 and size % 4 == 0
+    # 256 (sequence, KV head) units x 2,048 blocks / 4,096 -> 128-block splits, 16 per row:
+    # FP32 partials [32, 32, 16, 128 + 2].
+    assert size == 32 * 32 * 16 * (128 + 2) * 4
     bad = _lib.DecodeShape(32, 30, 8, 128, 36, 16, 0, 2048, _lib.LK_BF16, _lib.LK_BF16, 1.0)
     assert kernels.lk_paged_decode_workspace(bad) == 0
+
+
+def test_fp8_append_refuses_bad_arguments_without_launching():
+    kernels = _lib.load()
+    one = ctypes.c_int32(0)
+    ptr = ctypes.addressof(one)
+    assert kernels.lk_fp8_append(None, ptr, ptr, 1, 1, ptr, ptr, 0, 36, 8, 16, 128, None) == _lib.LK_ERR_INVALID
+    assert b"null" in kernels.lk_last_error()
+    assert kernels.lk_fp8_append(ptr, ptr, ptr, 1, 1, ptr, ptr, 36, 36, 8, 16, 128, None) == _lib.LK_ERR_INVALID
+    assert b"layer" in kernels.lk_last_error()
+    assert kernels.lk_fp8_append(ptr, ptr, ptr, 0, 1, ptr, ptr, 0, 36, 8, 16, 128, None) == _lib.LK_ERR_INVALID
+    assert kernels.lk_fp8_append(ptr, ptr, ptr, 1, 1, ptr, ptr, 0, 36, 0, 16, 128, None) == _lib.LK_ERR_INVALID

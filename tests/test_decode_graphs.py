@@ -1,0 +1,117 @@
+"""CPU side of the decode-step data path: the oracle's FP8 append (pinned against the record
+quantizer, which test_oracle.py pins against the reference's codec) and the bookkeeping of
+DecodeAttentionGraphs (reference layover/decode_graphs.py: sizes, padding rows on a reserved
+scratch block, fixed table width). Replays themselves run in tests/test_gpu_graphs.py."""
+
+import numpy as np
+import pytest
+import torch
+
+from layover_amd.config import ModelConfig
+from layover_amd.kv.decode_graphs import DecodeAttentionGraphs
+from layover_amd.kv.paged_cache import BlockTable, PagedKVCache
+from oracle import oracle
+
+LAYERS, HEADS, SLOTS, DIM = 2, 2, 16, 24
+GROUP, GROUPS = SLOTS * DIM, 2 * LAYERS * HEADS
+
+
+def quantized_blocks(blocks, seed):
+    bits = oracle.bf16_bits(np.random.default_rng(seed).standard_normal((blocks, 2, LAYERS, HEADS, SLOTS, DIM), dtype=np.float32))
+    return bits, oracle.quantize_records(bits, list(range(blocks)), GROUP, GROUPS).reshape(blocks, -1)
+
+
+def tokens(rows, seed, scale=1.0):
+    return oracle.bf16_bits(np.random.default_rng(seed).standard_normal((rows, HEADS, DIM), dtype=np.float32) * scale)
+
+
+def test_append_into_an_empty_block_quantizes_just_that_token():
+    records = np.zeros((1, GROUP * GROUPS + 2 * GROUPS), dtype=np.uint8)
+    k, v = tokens(1, 1, 9.0), tokens(1, 2, 0.01)
+    got = oracle.append_tokens(records, LAYERS, HEADS, SLOTS, DIM, [0], [0], 1, k, v)
+    block = np.zeros((1, 2, LAYERS, HEADS, SLOTS, DIM), dtype=np.uint16)
+    block[0, 0, 1, :, 0], block[0, 1, 1, :, 0] = k[0], v[0]
+    assert np.array_equal(got[0], oracle.quantize_records(block, [0], GROUP, GROUPS))
+
+
+def test_append_that_keeps_every_shift_leaves_earlier_codes_and_other_layers_alone():
+    _, records = quantized_blocks(3, 3)
+    k, v = tokens(1, 4, 0.5), tokens(1, 5, 0.5)  # small: cannot raise a group's largest exponent
+    got = oracle.append_tokens(records, LAYERS, HEADS, SLOTS, DIM, [2], [9], 0, k, v)
+    assert np.array_equal(got[:2], records[:2])
+    block_elems = GROUP * GROUPS
+    for kind in (0, 1):
+        for head in range(HEADS):
+            g = (kind * LAYERS + 0) * HEADS + head
+            codes, old = got[2, g * GROUP : (g + 1) * GROUP], records[2, g * GROUP : (g + 1) * GROUP]
+            assert np.array_equal(codes[: 9 * DIM], old[: 9 * DIM])  # earlier slots: same codes
+            assert not codes[10 * DIM :].any()  # later slots: zero
+            assert np.array_equal(got[2, block_elems + 2 * g : block_elems + 2 * g + 2], records[2, block_elems + 2 * g : block_elems + 2 * g + 2])
+    untouched = [g for g in range(GROUPS) if (g // HEADS) % LAYERS != 0]
+    for g in untouched:
+        assert np.array_equal(got[2, g * GROUP : (g + 1) * GROUP], records[2, g * GROUP : (g + 1) * GROUP])
+
+
+def test_append_that_raises_the_largest_exponent_requantizes_the_group():
+    bits, records = quantized_blocks(1, 6)
+    k = tokens(1, 7, 1000.0)
+    got = oracle.append_tokens(records, LAYERS, HEADS, SLOTS, DIM, [0], [15], 1, k, tokens(1, 8))
+    block_elems = GROUP * GROUPS
+    g = (0 * LAYERS + 1) * HEADS + 0
+    shift = got[0, block_elems + 2 * g : block_elems + 2 * g + 2].view(np.int16)[0]
+    restored = np.zeros((1, GROUP), dtype=np.uint16)
+    restored[0, : 15 * DIM] = oracle.decode(records[0, g * GROUP : g * GROUP + 15 * DIM],
+                                            int(records[0, block_elems + 2 * g : block_elems + 2 * g + 2].view(np.int16)[0]))
+    restored[0, 15 * DIM :] = k[0, 0]
+    assert shift == oracle.group_shifts(restored)[0] > records[0, block_elems + 2 * g : block_elems + 2 * g + 2].view(np.int16)[0]
+    assert np.array_equal(got[0, g * GROUP : (g + 1) * GROUP], oracle.encode(restored[0], int(shift)))
+
+
+def stub_capture(step, pool=None):
+    return (lambda: None), None, pool
+
+
+def test_graph_bookkeeping_reserves_a_scratch_block_and_pads_with_it():
+    cache = PagedKVCache(ModelConfig.micro(), 12, fill=False)
+    graphs = DecodeAttentionGraphs(cache, 4, sizes=(4, 1, 2), max_tokens=100, capture=stub_capture)
+    assert graphs.sizes == (1, 2, 4) and graphs.width == 7
+    assert cache.allocator.refcount(graphs.scratch) == 1
+    assert [graphs.size_for(n) for n in (1, 2, 3, 4, 5)] == [1, 2, 4, 4, None]
+    padding = graphs._padding(2)
+    assert padding.tolist() == [[graphs.scratch, 0, 1, graphs.scratch, 0, 0, 0, 0, 0, 0]] * 2
+    assert graphs.packed.shape == (4, 10) and torch.equal(graphs.packed, padding.repeat(2, 1))
+    assert graphs.q.shape == (2, 4, 4, 24) and graphs.k_new.shape == (2, 4, 2, 24)
+    assert set(graphs._workspaces) == {1, 2, 4}
+
+
+def test_graphs_decline_batches_and_tables_they_were_not_captured_for():
+    cache = PagedKVCache(ModelConfig.micro(), 12, fill=False)
+    graphs = DecodeAttentionGraphs(cache, 4, sizes=(1, 2), max_tokens=32, capture=stub_capture)
+    q, kv = torch.zeros(2, 3, 4, 24), torch.zeros(2, 3, 2, 24)
+    assert graphs.run([BlockTable([1], 3)] * 3, q, kv, kv) is None
+    assert graphs.run([BlockTable([1, 2, 3], 40)], q[:, :1], kv[:, :1], kv[:, :1]) is None
+
+
+def test_graphs_refuse_a_head_count_that_does_not_divide():
+    with pytest.raises(ValueError, match="divide"):
+        DecodeAttentionGraphs(PagedKVCache(ModelConfig.micro(), 4, fill=False), 3, capture=stub_capture)
+
+
+def test_decode_launch_layout_takes_packed_columns_and_refuses_what_it_cannot_describe():
+    from layover_amd.kernels import hip_decode
+
+    cache = PagedKVCache(ModelConfig.micro(), 12, fill=False)
+    packed = cache.decode_rows([BlockTable([3, 7], 20), BlockTable([5], 1), BlockTable([1, 2, 9], 48)])
+    table, lengths = packed[:, 3:], packed[:, 2]
+    q = torch.zeros(3, 4, 24, dtype=torch.bfloat16)
+    hip_decode._check_layout(q, table, lengths, q.clone())
+    shape = hip_decode.decode_shape(q, cache.pool, 1, table, 2, lengths)
+    assert (shape.table_width, shape.table_stride, shape.lengths_stride) == (3, 6, 6)
+    with pytest.raises(ValueError, match="rows must be contiguous"):
+        hip_decode._check_layout(q, packed.t().contiguous().t()[:, 3:], lengths, q.clone())
+    with pytest.raises(ValueError, match="int32"):
+        hip_decode._check_layout(q, table.long(), lengths, q.clone())
+    with pytest.raises(ValueError, match="batch"):
+        hip_decode._check_layout(q, table, lengths[:2], q.clone())
+    with pytest.raises(ValueError, match="contiguous tensors"):
+        hip_decode._check_layout(q, table, lengths, q.transpose(0, 1).contiguous().transpose(0, 1))

@@ -1,0 +1,239 @@
+"""The FP8-resident pool's decode-time write (lk_fp8_append) and HIP-graph decode steps on the
+GPU, through the C ABI.
+
+Appends are bit-exact against oracle.append_tokens, which is built only from the oracle's
+record quantize/dequantize (pinned against the reference's codec in test_oracle.py), and an
+append into an empty block equals quantizing a BF16 block that holds just that token. Graph
+replays are checked bit for bit against the eager step on the same buffers, several replays
+with other eager work between them, and against the float64 oracle decode (reference
+decode_graphs.py behaviour; tolerance as the other decode tests)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+QWEN_LIKE = dict(layers=36, kv_heads=8, slots=16, head_dim=128)
+
+
+def random_records(blocks, layers, kv_heads, slots, head_dim, seed):
+    rng = np.random.default_rng(seed)
+    bits = oracle.bf16_bits(rng.standard_normal((blocks, 2, layers, kv_heads, slots, head_dim), dtype=np.float32))
+    group_elems, groups = slots * head_dim, 2 * layers * kv_heads
+    records = oracle.quantize_records(bits, list(range(blocks)), group_elems, groups).reshape(blocks, -1)
+    return records
+
+
+def fp8_pool(records, layers, kv_heads, slots, head_dim):
+    from layover_amd.kernels.hip_decode import Fp8KVPool
+
+    return Fp8KVPool(torch.from_numpy(records).cuda(), layers, kv_heads, slots, head_dim)
+
+
+@pytest.mark.parametrize("shape", [QWEN_LIKE, dict(layers=2, kv_heads=2, slots=16, head_dim=24), dict(layers=3, kv_heads=1, slots=5, head_dim=40)],
+                         ids=["qwen3_4b", "micro", "odd"])
+def test_fp8_append_is_bit_exact_against_the_oracle(shape):
+    blocks, rows = 12, 6
+    records = random_records(blocks, **shape, seed=1)
+    rng = np.random.default_rng(2)
+    write_blocks = rng.permutation(blocks)[:rows].astype(np.int32)
+    write_slots = rng.integers(0, shape["slots"], rows).astype(np.int32)
+    scale = np.ones((rows, shape["kv_heads"], 1), dtype=np.float32)
+    scale[::2] = 64.0  # half the rows raise their groups' largest exponent
+    k = oracle.bf16_bits(rng.standard_normal((rows, shape["kv_heads"], shape["head_dim"]), dtype=np.float32) * scale)
+    v = oracle.bf16_bits(rng.standard_normal((rows, shape["kv_heads"], shape["head_dim"]), dtype=np.float32) / scale)
+    k[1, 0, :3] = [0x7F80, 0xFFC0, 0x0001]  # infinity, NaN, a BF16 subnormal
+    pool = fp8_pool(records, **shape)
+    layer = shape["layers"] - 1
+    print(f"append {shape} layer {layer}", flush=True)
+    pool.write(torch.from_numpy(write_blocks).cuda(), torch.from_numpy(write_slots).cuda(), layer,
+               torch.from_numpy(k.view(np.int16)).cuda().view(torch.bfloat16), torch.from_numpy(v.view(np.int16)).cuda().view(torch.bfloat16))
+    expected = oracle.append_tokens(records, shape["layers"], shape["kv_heads"], shape["slots"], shape["head_dim"], write_blocks,
+                                    write_slots, layer, k, v)
+    assert np.array_equal(pool.records.cpu().numpy(), expected)
+
+
+def test_fp8_append_into_an_empty_block_equals_quantizing_the_token():
+    shape = QWEN_LIKE
+    group_elems, groups = shape["slots"] * shape["head_dim"], 2 * shape["layers"] * shape["kv_heads"]
+    records = np.zeros((2, group_elems * groups + 2 * groups), dtype=np.uint8)
+    rng = np.random.default_rng(3)
+    k = oracle.bf16_bits(rng.standard_normal((1, 8, 128), dtype=np.float32) * 3)
+    v = oracle.bf16_bits(rng.standard_normal((1, 8, 128), dtype=np.float32) / 5)
+    pool = fp8_pool(records, **shape)
+    rows = torch.tensor([1], dtype=torch.int32, device="cuda")
+    pool.write(rows, torch.zeros_like(rows), 7, torch.from_numpy(k.view(np.int16)).cuda().view(torch.bfloat16),
+               torch.from_numpy(v.view(np.int16)).cuda().view(torch.bfloat16))
+    block = np.zeros((1, 2, 36, 8, 16, 128), dtype=np.uint16)
+    block[0, 0, 7, :, 0] = k[0]
+    block[0, 1, 7, :, 0] = v[0]
+    quantized = oracle.quantize_records(block, [0], group_elems, groups)
+    got = pool.records.cpu().numpy()
+    assert np.array_equal(got[1], quantized) and not got[0].any()
+
+
+def test_fp8_append_reads_rows_from_decode_row_columns():
+    from layover_amd.config import ModelConfig
+    from layover_amd.kv.paged_cache import BlockTable, PagedKVCache
+
+    cache = PagedKVCache(ModelConfig.micro(), 10, fill=False)
+    tables = [BlockTable([3, 7], 20), BlockTable([5], 1), BlockTable([1, 2, 9], 48)]
+    packed = cache.decode_rows(tables).cuda()
+    records = random_records(10, layers=2, kv_heads=2, slots=16, head_dim=24, seed=4)
+    pool = fp8_pool(records, layers=2, kv_heads=2, slots=16, head_dim=24)
+    rng = np.random.default_rng(5)
+    k = oracle.bf16_bits(rng.standard_normal((3, 2, 24), dtype=np.float32))
+    v = oracle.bf16_bits(rng.standard_normal((3, 2, 24), dtype=np.float32))
+    pool.write(packed[:, 0], packed[:, 1], 1, torch.from_numpy(k.view(np.int16)).cuda().view(torch.bfloat16),
+               torch.from_numpy(v.view(np.int16)).cuda().view(torch.bfloat16))
+    expected = oracle.append_tokens(records, 2, 2, 16, 24, [7, 5, 9], [3, 0, 15], 1, k, v)
+    assert np.array_equal(pool.records.cpu().numpy(), expected)
+
+
+def test_fp8_append_refuses_bad_tensors():
+    pool = fp8_pool(np.zeros((2, 2 * 2 * 2 * 16 * 24 + 16), dtype=np.uint8), layers=2, kv_heads=2, slots=16, head_dim=24)
+    rows = torch.zeros(1, dtype=torch.int32, device="cuda")
+    k = torch.zeros(1, 2, 24, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(ValueError, match="layer"):
+        pool.write(rows, rows, 2, k, k)
+    with pytest.raises(ValueError, match="int32"):
+        pool.write(rows.long(), rows, 0, k, k)
+    with pytest.raises(ValueError, match="BF16"):
+        pool.write(rows, rows, 0, k.float(), k)
+
+
+def decode_reference(pool_bits, q, tables_rows, groups):
+    """float64 oracle attention for every layer over rows [write block, slot, length, table...]."""
+    rows = np.asarray(tables_rows)
+    table, lengths = rows[:, 3:], rows[:, 2]
+    layers = pool_bits.shape[2]
+    return np.stack([oracle.decode_attention(q[layer], pool_bits, layer, table, lengths, groups) for layer in range(layers)])
+
+
+def assert_close(got, reference):
+    got = got.float().cpu().numpy().astype(np.float64)
+    # BF16 output rounding plus FP32 accumulation, as in the other decode tests.
+    assert np.all(np.abs(got - reference) <= 2.0**-8 * np.abs(reference) + 1e-3), np.abs(got - reference).max()
+
+
+@pytest.mark.parametrize("fp8", [False, True], ids=["bf16_pool", "fp8_pool"])
+def test_graph_replays_equal_the_eager_step_and_the_oracle(fp8):
+    from layover_amd.config import ModelConfig
+    from layover_amd.kernels import hip_decode
+    from layover_amd.kv.decode_graphs import DecodeAttentionGraphs
+    from layover_amd.kv.paged_cache import BlockTable, PagedKVCache
+
+    cfg = ModelConfig.qwen3_4b()
+    cache = PagedKVCache(cfg, 48, device="cuda", fill=False)
+    rng = np.random.default_rng(6)
+    bits = oracle.bf16_bits(rng.standard_normal(cache.pool.shape, dtype=np.float32))
+    cache.pool.copy_(torch.from_numpy(bits.view(np.int16)).cuda().view(torch.bfloat16))
+    pool = None
+    if fp8:
+        group_elems, groups = 16 * 128, 2 * 36 * 8
+        records = oracle.quantize_records(bits, list(range(48)), group_elems, groups).reshape(48, -1)
+        pool = fp8_pool(records, **QWEN_LIKE)
+    print(f"graphs fp8={fp8}", flush=True)
+    graphs = DecodeAttentionGraphs(cache, 32, pool=pool, sizes=(1, 4), max_tokens=16 * 20)
+    ids = [b for b in rng.permutation(48).tolist() if b != graphs.scratch]
+    tables = [BlockTable(ids[0:20], 20 * 16), BlockTable(ids[20:21], 1), BlockTable(ids[21:24], 35)]
+    q = torch.randn(36, 3, 32, 128, device="cuda").to(torch.bfloat16)
+    k_new = torch.randn(36, 3, 8, 128, device="cuda").to(torch.bfloat16)
+    v_new = torch.randn(36, 3, 8, 128, device="cuda").to(torch.bfloat16)
+    out = graphs.run(tables, q, k_new, v_new)
+    torch.cuda.synchronize()
+    assert out.shape == (36, 3, 32, 128)
+
+    # The pool after the step, as the oracle sees it.
+    if fp8:
+        state = np.zeros_like(bits)
+        oracle.dequantize_records(pool.records.cpu().numpy().reshape(-1), list(range(48)), state, 16 * 128, 2 * 36 * 8)
+    else:
+        state = cache.pool.view(torch.int16).cpu().numpy().view(np.uint16)
+    rows = cache.decode_rows(tables, graphs.width).numpy()
+    if not fp8:  # the step wrote each row's new token (model.py:139-140)
+        for b, t in enumerate(rows):
+            for layer in (0, 35):
+                assert np.array_equal(state[t[0], 1, layer, :, t[1]], v_new[layer, b].view(torch.int16).cpu().numpy().view(np.uint16))
+    reference = decode_reference(state, q.float().cpu().numpy(), rows, 4)
+    assert_close(out, reference)
+
+    eager = graphs.step_eager(4)[:, :3].clone()
+    torch.cuda.synchronize()
+    assert torch.equal(eager.view(torch.int16), out.view(torch.int16))
+    for replay in range(3):
+        # Other eager work on the device between replays.
+        hip_decode.paged_decode_attention_hip(q[0], graphs.pool, 0, graphs.packed[:3, 3:], graphs.packed[:3, 2], 4)
+        torch.cuda.synchronize()
+        again = graphs.replay(4)[:, :3].clone()
+        torch.cuda.synchronize()
+        assert torch.equal(again.view(torch.int16), out.view(torch.int16)), f"replay {replay} differs"
+
+    assert graphs.run([BlockTable(ids[:1], 5)] * 5, q[:, :1].repeat(1, 5, 1, 1), k_new[:, :1].repeat(1, 5, 1, 1),
+                      v_new[:, :1].repeat(1, 5, 1, 1)) is None  # no graph for five rows
+    assert graphs.run([BlockTable(ids[:21], 21 * 16)], q[:, :1], k_new[:, :1], v_new[:, :1]) is None  # wider than captured
+
+
+@pytest.mark.parametrize("lengths", [[1], [16 * 64], [16 * 64 + 1], [32768], [5, 16 * 300, 17, 16 * 64 * 3 + 9]],
+                         ids=["one_token", "one_split", "two_splits", "batch1_32k", "mixed"])
+def test_combine_over_split_counts(lengths):
+    """Split-K at its edges: one split, exactly two, many, and mixed counts in one launch,
+    twice on one workspace (whatever the first call left there must not matter)."""
+    from layover_amd.kernels import hip_decode
+
+    blocks = sum(-(-n // 16) for n in lengths) + 1
+    rng = np.random.default_rng(len(lengths) + lengths[0])
+    pool_bits = oracle.bf16_bits(rng.standard_normal((blocks, 2, 2, 8, 16, 128), dtype=np.float32))
+    pool = torch.from_numpy(pool_bits.view(np.int16)).cuda().view(torch.bfloat16)
+    width = max(-(-n // 16) for n in lengths)
+    table = np.zeros((len(lengths), width), dtype=np.int32)
+    ids = rng.permutation(blocks)
+    at = 0
+    for b, n in enumerate(lengths):
+        table[b, : -(-n // 16)] = ids[at : at + -(-n // 16)]
+        at += -(-n // 16)
+    q = torch.randn(len(lengths), 32, 128, device="cuda").to(torch.bfloat16)
+    t, lens = torch.from_numpy(table).cuda(), torch.tensor(lengths, dtype=torch.int32, device="cuda")
+    shape = hip_decode.decode_shape(q, pool, 1, t, 4)
+    workspace = torch.full((hip_decode.workspace_bytes(shape),), 0xFF, dtype=torch.uint8, device="cuda")
+    out = torch.empty_like(q)
+    reference = oracle.decode_attention(q.float().cpu().numpy(), pool_bits, 1, table, np.array(lengths), 4)
+    for call in range(2):
+        hip_decode.run_kernel(q, pool, 1, t, lens, 4, out, workspace)
+        torch.cuda.synchronize()
+        assert_close(out, reference)
+
+
+@pytest.mark.parametrize("fp8", [False, True], ids=["bf16_pool", "fp8_pool"])
+def test_decode_reads_packed_row_columns_by_stride(fp8):
+    """The table and lengths as column views of decode_rows' packed block (row stride 3 +
+    width) give the same output as contiguous copies, and match the oracle."""
+    from layover_amd.config import ModelConfig
+    from layover_amd.kernels import hip_decode
+    from layover_amd.kv.paged_cache import BlockTable, PagedKVCache
+
+    cache = PagedKVCache(ModelConfig.qwen3_4b(), 40, fill=False)
+    rng = np.random.default_rng(9)
+    bits = oracle.bf16_bits(rng.standard_normal(cache.pool.shape, dtype=np.float32))
+    ids = rng.permutation(40).tolist()
+    tables = [BlockTable(ids[0:9], 130), BlockTable(ids[9:10], 3), BlockTable(ids[10:30], 20 * 16), BlockTable(ids[30:31], 16)]
+    packed = cache.decode_rows(tables).cuda()
+    if fp8:
+        pool = fp8_pool(oracle.quantize_records(bits, list(range(40)), 16 * 128, 576).reshape(40, -1), **QWEN_LIKE)
+        state = np.zeros_like(bits)
+        oracle.dequantize_records(pool.records.cpu().numpy().reshape(-1), list(range(40)), state, 16 * 128, 576)
+    else:
+        pool = torch.from_numpy(bits.view(np.int16)).cuda().view(torch.bfloat16)
+        state = bits
+    q = torch.randn(4, 32, 128, device="cuda").to(torch.bfloat16)
+    strided, contiguous = torch.empty_like(q), torch.empty_like(q)
+    print(f"strided decode fp8={fp8}", flush=True)
+    hip_decode.run_kernel(q, pool, 20, packed[:, 3:], packed[:, 2], 4, strided)
+    hip_decode.run_kernel(q, pool, 20, packed[:, 3:].contiguous(), packed[:, 2].contiguous(), 4, contiguous)
+    torch.cuda.synchronize()
+    assert torch.equal(strided.view(torch.int16), contiguous.view(torch.int16))
+    rows = packed.cpu().numpy()
+    assert_close(strided, oracle.decode_attention(q.float().cpu().numpy(), state, 20, rows[:, 3:], rows[:, 2], 4))

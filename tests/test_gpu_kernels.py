@@ -39,7 +39,7 @@ def test_kernel_library_loads_into_torchs_hip_runtime():
 
     torch.zeros(1, device="cuda")
     lib = _lib.load()
-    assert lib.lk_abi_version() == 1
+    assert lib.lk_abi_version() == 2
     assert load_library("hip").lt_flavor() == b"hip"
     assert len(hip_runtimes_loaded()) == 1, hip_runtimes_loaded()
 
