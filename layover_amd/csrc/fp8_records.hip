@@ -32,12 +32,8 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float power_of_two(int32_t e) { return __uint_as_float(uint32_t(e + 127) << 23); }
 
-__global__ __launch_bounds__(kWave* kCodecWaves) void quantize_groups_2048(const uint16_t* __restrict__ pool,
-                                                                         const int32_t* __restrict__ ids, uint8_t* __restrict__ stage,
-                                                                         uint32_t count, uint32_t groups_per_block) {
-    const uint32_t lane = threadIdx.x % kWave;
-    const uint64_t group = uint64_t(blockIdx.x) * kCodecWaves + threadIdx.x / kWave;
-    if (group >= uint64_t(count) * groups_per_block) return;
+__device__ __forceinline__ void quantize_group(const uint16_t* __restrict__ pool, const int32_t* __restrict__ ids, uint8_t* __restrict__ stage,
+                                               uint32_t groups_per_block, uint64_t group, uint32_t lane) {
     const uint32_t index = uint32_t(group / groups_per_block);
     const uint32_t g = uint32_t(group % groups_per_block);
     const uint64_t block_elems = uint64_t(kFastGroup) * groups_per_block;
@@ -94,12 +90,18 @@ __global__ __launch_bounds__(kWave* kCodecWaves) void quantize_groups_2048(const
     if (lane == 0) *reinterpret_cast<int16_t*>(out + block_elems + 2ull * g) = int16_t(shift);
 }
 
-__global__ __launch_bounds__(kWave* kCodecWaves) void dequantize_groups_2048(const uint8_t* __restrict__ stage,
-                                                                           const int32_t* __restrict__ ids, uint16_t* __restrict__ pool,
-                                                                           uint32_t count, uint32_t groups_per_block) {
+__global__ __launch_bounds__(kWave* kCodecWaves) void quantize_groups_2048(const uint16_t* __restrict__ pool,
+                                                                         const int32_t* __restrict__ ids, uint8_t* __restrict__ stage,
+                                                                         uint32_t count, uint32_t groups_per_block) {
     const uint32_t lane = threadIdx.x % kWave;
-    const uint64_t group = uint64_t(blockIdx.x) * kCodecWaves + threadIdx.x / kWave;
-    if (group >= uint64_t(count) * groups_per_block) return;
+    const uint64_t total = uint64_t(count) * groups_per_block;
+    const uint64_t stride = uint64_t(gridDim.x) * kCodecWaves;
+    for (uint64_t group = uint64_t(blockIdx.x) * kCodecWaves + threadIdx.x / kWave; group < total; group += stride)
+        quantize_group(pool, ids, stage, groups_per_block, group, lane);
+}
+
+__device__ __forceinline__ void dequantize_group(const uint8_t* __restrict__ stage, const int32_t* __restrict__ ids, uint16_t* __restrict__ pool,
+                                                 uint32_t groups_per_block, uint64_t group, uint32_t lane) {
     const uint32_t index = uint32_t(group / groups_per_block);
     const uint32_t g = uint32_t(group % groups_per_block);
     const uint64_t block_elems = uint64_t(kFastGroup) * groups_per_block;
@@ -146,6 +148,16 @@ __global__ __launch_bounds__(kWave* kCodecWaves) void dequantize_groups_2048(con
             target[j * kWave + lane] = out;
         }
     }
+}
+
+__global__ __launch_bounds__(kWave* kCodecWaves) void dequantize_groups_2048(const uint8_t* __restrict__ stage,
+                                                                           const int32_t* __restrict__ ids, uint16_t* __restrict__ pool,
+                                                                           uint32_t count, uint32_t groups_per_block) {
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint64_t total = uint64_t(count) * groups_per_block;
+    const uint64_t stride = uint64_t(gridDim.x) * kCodecWaves;
+    for (uint64_t group = uint64_t(blockIdx.x) * kCodecWaves + threadIdx.x / kWave; group < total; group += stride)
+        dequantize_group(stage, ids, pool, groups_per_block, group, lane);
 }
 
 void launch_quantize_2048(const uint16_t* pool, const int32_t* ids, uint8_t* stage, uint32_t count, uint32_t groups_per_block,
