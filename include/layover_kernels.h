@@ -10,6 +10,10 @@
  *   lk_paged_decode    layover/kernels/triton_decode.py:131-179 kernel_launch/run_kernel
  *                      (_paged_decode_kernel :39-119); the FP8-record KV format has no
  *                      reference counterpart (the reference decodes BF16 and FP32 pools only).
+ *   lk_paged_prefill   layover/model.py:69-98 prefill_attention (gather + FlashAttention),
+ *                      read in place instead of gathered.
+ *   lk_fp8_append      no counterpart: the FP8-resident pool's version of the decode-time
+ *                      pool write of layover/model.py:139-140.
  *
  * Conventions: plain device pointers and sizes; `stream` is a hipStream_t (a torch stream's
  * cuda_stream; null means the legacy default stream). Every entry point only enqueues work
@@ -95,6 +99,31 @@ uint64_t lk_paged_decode_workspace(const lk_decode_shape* shape);
  * table_width*slots and every id in range, which the caller has checked. */
 int lk_paged_decode(const lk_decode_shape* shape, const void* q, const void* pool, const int32_t* table,
                     const int32_t* lengths, void* out, void* workspace, uint64_t workspace_bytes, void* stream);
+
+/* One prefill chunk of one sequence and one layer, causal: query token t of the chunk (absolute
+ * position start + t) attends to keys 0 .. start + t, read in place from the pool through
+ * block_ids (int32, the sequence's blocks in order; at least ceil((start + tokens) / slots)
+ * of them, num_block_ids given for the check). q and out are BF16 [query_heads, tokens,
+ * head_dim]; query head h reads KV head h / (query_heads / kv_heads). The chunk's own K/V
+ * must already be in the pool. Replaces the reference's gather + FlashAttention
+ * (layover/model.py:69-98, prefill_attention). Supported: 16 slots x 128 dims, BF16 q, BF16
+ * or FP8-record pools. */
+typedef struct {
+    uint32_t tokens;      /* query tokens in the chunk */
+    uint32_t start;       /* position of the chunk's first token */
+    uint32_t query_heads;
+    uint32_t kv_heads;
+    uint32_t head_dim;
+    uint32_t layers;
+    uint32_t slots;
+    uint32_t layer;
+    int32_t q_format;     /* LK_BF16 */
+    int32_t kv_format;    /* LK_BF16 or LK_FP8_RECORD */
+    float scale;
+} lk_prefill_shape;
+
+int lk_paged_prefill(const lk_prefill_shape* shape, const void* q, const void* pool, const int32_t* block_ids, uint32_t num_block_ids,
+                     void* out, void* stream);
 
 /* One decode step's KV write into an FP8-record pool: no reference counterpart (the
  * reference writes BF16 tokens into a BF16 pool, layover/model.py:139-140). For row b,

@@ -9,6 +9,7 @@
 #include <string>
 
 #include "decode_attention.h"
+#include "prefill_attention.h"
 #include "fp8_codec.h"
 #include "layover_kernels.h"
 
@@ -470,6 +471,57 @@ LK_EXPORT int lk_paged_decode(const lk_decode_shape* shape, const void* q, const
         auto st = static_cast<hipStream_t>(stream);
         if (s.q_format == LK_BF16) lk::launch_decode<LK_BF16>(a, g, s.kv_format, out, st);
         else lk::launch_decode<LK_F32>(a, g, s.kv_format, out, st);
+    });
+}
+
+LK_EXPORT int lk_paged_prefill(const lk_prefill_shape* shape, const void* q, const void* pool, const int32_t* block_ids,
+                               uint32_t num_block_ids, void* out, void* stream) {
+    return lk::guarded([&] {
+        lk::require(shape != nullptr, "null shape");
+        const lk_prefill_shape& s = *shape;
+        lk::require(q && pool && block_ids && out, "null q, pool, block ids or out");
+        lk::require(s.tokens > 0 && s.query_heads > 0 && s.kv_heads > 0 && s.layers > 0, "every prefill dimension must be positive");
+        lk::require(s.query_heads % s.kv_heads == 0, "query heads must be a multiple of KV heads");
+        lk::require(s.layer < s.layers, "layer out of range");
+        lk::require(s.slots == lk::kSlots && s.head_dim == lk::kDim, "paged prefill supports 16-slot blocks of 128 dims");
+        lk::require(s.q_format == LK_BF16, "paged prefill takes BF16 q");
+        lk::require(s.kv_format == LK_BF16 || s.kv_format == LK_FP8_RECORD, "paged prefill reads BF16 or FP8-record pools");
+        const uint64_t end = uint64_t(s.start) + s.tokens;
+        lk::require(uint64_t(num_block_ids) * s.slots >= end, "fewer block ids than the chunk's end needs");
+        lk_decode_shape d{};
+        d.layers = s.layers;
+        d.kv_heads = s.kv_heads;
+        d.slots = s.slots;
+        d.head_dim = s.head_dim;
+        d.kv_format = s.kv_format;
+        const uint64_t block_bytes = lk::pool_block_bytes(d);
+        lk::require(lk::aligned(q, 16) && lk::aligned(out, 16) && lk::aligned(pool, 16) && block_bytes % 16 == 0,
+                    "q, out and pool blocks must be 16-byte aligned");
+        const uint32_t groups = s.query_heads / s.kv_heads;
+        const uint64_t rows = uint64_t(s.tokens) * groups;
+        const uint64_t row_tiles = (rows + lk::kPrefillRows * lk::kPrefillWaves - 1) / (lk::kPrefillRows * lk::kPrefillWaves);
+        const uint64_t grid = row_tiles * s.kv_heads;
+        lk::require(rows <= 0xFFFFFFFFull && grid <= 0x7FFFFFFFull, "prefill chunk too large for one launch");
+        lk::PrefillArgs a{};
+        a.q = static_cast<const uint16_t*>(q);
+        a.pool = static_cast<const uint8_t*>(pool);
+        a.block_ids = block_ids;
+        a.out = static_cast<uint16_t*>(out);
+        a.tokens = s.tokens;
+        a.start = s.start;
+        a.query_heads = s.query_heads;
+        a.kv_heads = s.kv_heads;
+        a.groups = groups;
+        a.layers = s.layers;
+        a.layer = s.layer;
+        a.row_tiles = uint32_t(row_tiles);
+        a.block_bytes = block_bytes;
+        a.scale_log2 = s.scale * lk::kLog2e;
+        auto st = static_cast<hipStream_t>(stream);
+        if (s.kv_format == LK_BF16)
+            hipLaunchKernelGGL(lk::prefill_mfma<LK_BF16>, dim3(uint32_t(grid)), dim3(lk::kWave * lk::kPrefillWaves), 0, st, a);
+        else
+            hipLaunchKernelGGL(lk::prefill_mfma<LK_FP8_RECORD>, dim3(uint32_t(grid)), dim3(lk::kWave * lk::kPrefillWaves), 0, st, a);
     });
 }
 

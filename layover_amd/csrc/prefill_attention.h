@@ -1,0 +1,266 @@
+// Paged causal prefill attention on gfx950: a chunk of query tokens [start, start + tokens) of
+// one sequence attends to every key [0, start + t] through the sequence's block ids, read in
+// place from the pool (BF16 or FP8 records). The reference gathers the history out of the
+// pool once per layer and runs FlashAttention with a bottom-right causal mask
+// (layover/model.py:69-98; "reading it in place needs a paged prefill kernel"); the math here
+// is the same causal softmax attention, with FP32 accumulation.
+//
+// Work: query rows are (token, query head) pairs of one KV head, head fastest, so the G heads
+// sharing a KV head sit in adjacent rows. A wave owns 16 rows and walks the key blocks (16
+// slots each) up to its last row's causal limit, on the matrix cores exactly as the decode
+// kernel does for one block (decode_attention.h): S^T = K Q^T with v_mfma_f32_16x16x32_bf16
+// (lane (g, n): keys 4g..4g+3 of row n), an online softmax per row with the lazy 2^8 rescale,
+// and O += P V with v_mfma_f32_16x16x16_bf16 (lane (g, n): rows 4g..4g+3, dims 8n + e of
+// MFMA e). P enters the MFMA as one BF16 (not the decode kernel's hi + lo pair): relative
+// error about 2^-9 per weight, against the north-star tolerance of 1e-2. Keys past a row's
+// limit score -inf; V of slots at or past the chunk's end is zeroed, since those slots can
+// hold anything (0 * NaN is NaN).
+// Workgroups: 4 waves = 64 rows. Launch order: KV head fastest, and the heaviest row tiles
+// (latest tokens, most keys) first. With 8 KV heads the round-robin dealing of workgroups
+// onto the 8 XCDs then keeps each KV head's workgroups on one XCD, whose L2 holds that
+// head's K/V for all of them.
+#ifndef LAYOVER_AMD_PREFILL_ATTENTION_H
+#define LAYOVER_AMD_PREFILL_ATTENTION_H
+
+#include "decode_attention.h"
+
+namespace lk {
+
+constexpr uint32_t kPrefillWaves = 4;
+constexpr uint32_t kPrefillRows = 16;  // rows per wave
+
+struct PrefillArgs {
+    const uint16_t* q;         // BF16 [query_heads, tokens, 128]
+    const uint8_t* pool;
+    const int32_t* block_ids;  // the sequence's blocks, at least ceil((start + tokens) / 16)
+    uint16_t* out;             // BF16 [query_heads, tokens, 128]
+    uint32_t tokens, start, query_heads, kv_heads, groups, layers, layer;
+    uint32_t row_tiles;        // workgroups per KV head
+    uint64_t block_bytes;
+    float scale_log2;
+};
+
+template <int KV>
+__global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_mfma(PrefillArgs a) {
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const uint32_t g = lane / 16;
+    const uint32_t n = lane % 16;
+    const uint32_t kv_head = blockIdx.x % a.kv_heads;
+    const uint32_t tile = a.row_tiles - 1 - blockIdx.x / a.kv_heads;
+    const uint32_t total_rows = a.tokens * a.groups;
+    const uint32_t row0 = (tile * kPrefillWaves + wave) * kPrefillRows;
+    if (row0 >= total_rows) return;
+
+    // This lane's row n: its token, query head, and causal limit (last key position it sees).
+    const uint32_t row = row0 + n;
+    const bool live = row < total_rows;
+    const uint32_t token = live ? row / a.groups : 0;
+    const uint32_t head = kv_head * a.groups + (live ? row % a.groups : 0);
+    const int64_t limit = live ? int64_t(a.start) + token : -1;
+    const uint32_t last_row = min(row0 + kPrefillRows, total_rows) - 1;
+    const uint32_t end = a.start + a.tokens;
+    const uint32_t key_blocks = (a.start + last_row / a.groups) / kSlots + 1;
+
+    // B operand of QK: row n, dims 32g .. 32g+31 (step j takes dims 32g + 8j .. +8).
+    uint32_t qt[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) qt[i] = 0;
+    if (live) {
+        const u32x4* src = reinterpret_cast<const u32x4*>(a.q + (uint64_t(head) * a.tokens + token) * kDim + 32 * g);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const u32x4 w = src[j];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) qt[4 * j + i] = w[i];
+        }
+    }
+
+    constexpr uint32_t kElem = KV == LK_FP8_RECORD ? 1 : 2;
+    const uint64_t tile_bytes = uint64_t(kSlots) * kDim * kElem;
+    const uint64_t head_tile = uint64_t(a.layer) * a.kv_heads + kv_head;
+    const uint64_t k_offset = head_tile * tile_bytes + (uint64_t(n) * kDim + 32 * g) * kElem;
+    const uint64_t v_offset = (uint64_t(a.layers) * a.kv_heads + head_tile) * tile_bytes + (uint64_t(4 * g) * kDim + 8 * n) * kElem;
+    const uint64_t block_elems = uint64_t(2) * a.layers * a.kv_heads * kSlots * kDim;
+
+    auto fetch = [&](MfmaTile<KV>& t, uint32_t kb) {
+        const int32_t block = a.block_ids[kb];  // uniform: a scalar load
+        const uint8_t* base = a.pool + uint64_t(uint32_t(block)) * a.block_bytes;
+        if constexpr (KV == LK_BF16) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const u32x4 w = reinterpret_cast<const u32x4*>(base + k_offset)[j];
+#pragma unroll
+                for (int x = 0; x < 4; ++x) t.k[4 * j + x] = w[x];
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const u32x4 w = *reinterpret_cast<const u32x4*>(base + v_offset + uint64_t(r) * kDim * kElem);
+#pragma unroll
+                for (int x = 0; x < 4; ++x) t.v[r][x] = w[x];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const u32x4 w = reinterpret_cast<const u32x4*>(base + k_offset)[j];
+#pragma unroll
+                for (int x = 0; x < 4; ++x) t.k[4 * j + x] = w[x];
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const u32x2 w = *reinterpret_cast<const u32x2*>(base + v_offset + uint64_t(r) * kDim * kElem);
+                t.v[r][0] = w[0];
+                t.v[r][1] = w[1];
+            }
+            const int16_t* shifts = reinterpret_cast<const int16_t*>(base + block_elems);
+            t.k_shift = shifts[head_tile];
+            t.v_shift = shifts[uint64_t(a.layers) * a.kv_heads + head_tile];
+        }
+    };
+
+    float m = -INFINITY, l = 0.0f;
+    f32x4 o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto consume = [&](MfmaTile<KV>& t, uint32_t kb) {
+        const uint32_t key0 = kb * kSlots;
+        bool k_exact = false, v_exact = false;
+        float k_factor = a.scale_log2, v_factor = 1.0f;
+        if constexpr (KV == LK_FP8_RECORD) {
+            k_exact = !shift_is_exact_in_fp32(t.k_shift);
+            v_exact = !shift_is_exact_in_fp32(t.v_shift);
+            if (!k_exact) k_factor *= pow2(t.k_shift);
+            if (!v_exact) v_factor = pow2(t.v_shift);
+        }
+        uint32_t kb_[16];
+        uint32_t v[4][4];
+        if constexpr (KV == LK_BF16) {
+#pragma unroll
+            for (int x = 0; x < 16; ++x) kb_[x] = t.k[x];
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int x = 0; x < 4; ++x) v[r][x] = t.v[r][x];
+        } else {
+            if (__builtin_expect(k_exact || v_exact, 0)) {
+                asm volatile("" ::: "memory");
+#pragma unroll
+                for (int x = 0; x < 8; ++x) {
+                    kb_[2 * x] = fp8_pair(t.k[x], false, k_exact, t.k_shift);
+                    kb_[2 * x + 1] = fp8_pair(t.k[x], true, k_exact, t.k_shift);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int x = 0; x < 2; ++x) {
+                        v[r][2 * x] = fp8_pair(t.v[r][x], false, v_exact, t.v_shift);
+                        v[r][2 * x + 1] = fp8_pair(t.v[r][x], true, v_exact, t.v_shift);
+                    }
+            } else {
+#pragma unroll
+                for (int x = 0; x < 8; ++x) {
+                    kb_[2 * x] = fp8_pair(t.k[x], false, false, 0);
+                    kb_[2 * x + 1] = fp8_pair(t.k[x], true, false, 0);
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int x = 0; x < 2; ++x) {
+                        v[r][2 * x] = fp8_pair(t.v[r][x], false, false, 0);
+                        v[r][2 * x + 1] = fp8_pair(t.v[r][x], true, false, 0);
+                    }
+            }
+        }
+
+        f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kb_[4 * j], kb_[4 * j + 1], kb_[4 * j + 2], kb_[4 * j + 3]),
+                                                        as_bf16x8(qt[4 * j], qt[4 * j + 1], qt[4 * j + 2], qt[4 * j + 3]), s, 0, 0, 0);
+
+        float score[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) score[r] = int64_t(key0 + 4 * g + r) <= limit ? s[r] * k_factor : -INFINITY;
+        float top = fmaxf(fmaxf(score[0], score[1]), fmaxf(score[2], score[3]));
+        top = fmaxf(top, __shfl_xor(top, 16, kWave));
+        top = fmaxf(top, __shfl_xor(top, 32, kWave));
+        if (__builtin_expect(__any(top > m + kRescaleThreshold), 0)) {
+            asm volatile("" ::: "memory");
+            const float next = top > m + kRescaleThreshold ? top : m;
+            const float alpha = merge_weight(m, next);
+            m = next;
+            l *= alpha;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float factor = __shfl(alpha, int(4 * g + r), kWave);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[e][r] *= factor;
+            }
+        }
+        float p[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            p[r] = score[r] == -INFINITY ? 0.0f : exp2_fast(score[r] - m);
+            l += p[r];
+            p[r] *= v_factor;
+        }
+        const s16x4 pb = __builtin_bit_cast(s16x4, u32x2{pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3])});
+
+        if (key0 + kSlots > end) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const bool written = key0 + 4 * g + r < end;
+#pragma unroll
+                for (int x = 0; x < 4; ++x) v[r][x] = written ? v[r][x] : 0u;
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t select = (e & 1) ? 0x07060302u : 0x05040100u;
+            const uint32_t b01 = __builtin_amdgcn_perm(v[1][e / 2], v[0][e / 2], select);
+            const uint32_t b23 = __builtin_amdgcn_perm(v[3][e / 2], v[2][e / 2], select);
+            o[e] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pb, __builtin_bit_cast(s16x4, u32x2{b01, b23}), o[e], 0, 0, 0);
+        }
+    };
+
+    // Register ring, refilled unconditionally (see decode_split_mfma).
+    constexpr int kRing = KV == LK_BF16 ? LK_DECODE_RING_BF16 : LK_DECODE_RING_FP8;
+    MfmaTile<KV> ring[kRing];
+    const uint32_t last = key_blocks - 1;
+#pragma unroll
+    for (int d = 0; d < kRing; ++d) fetch(ring[d], min(uint32_t(d), last));
+    for (uint32_t i = 0; i < key_blocks; i += kRing) {
+#pragma unroll
+        for (int d = 0; d < kRing; ++d) {
+            if (i + d < key_blocks) consume(ring[d], i + d);
+            fetch(ring[d], min(i + d + kRing, last));
+        }
+    }
+
+    // Row n's weight sum over the four lane groups, then O rows 4g + r scaled by 1 / l of
+    // their row (held by lane 4g + r) and written as BF16, 16 bytes (dims 8n .. 8n+7) a row.
+    l += __shfl_xor(l, 16, kWave);
+    l += __shfl_xor(l, 32, kWave);
+    const float inverse = 1.0f / l;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float factor = __shfl(inverse, int(4 * g + r), kWave);
+        const uint32_t out_row = row0 + 4 * g + r;
+        if (out_row < total_rows) {
+            const uint32_t out_token = out_row / a.groups;
+            const uint32_t out_head = kv_head * a.groups + out_row % a.groups;
+            u32x4 packed;
+#pragma unroll
+            for (int x = 0; x < 4; ++x) {
+                const uint32_t lo = to_bf16(o[2 * x][r] * factor), hi = to_bf16(o[2 * x + 1][r] * factor);
+                packed[x] = lo | (hi << 16);
+            }
+            *reinterpret_cast<u32x4*>(a.out + (uint64_t(out_head) * a.tokens + out_token) * kDim + 8 * n) = packed;
+        }
+    }
+}
+
+}  // namespace lk
+
+#endif  // LAYOVER_AMD_PREFILL_ATTENTION_H

@@ -44,6 +44,22 @@ class DecodeShape(ctypes.Structure):
     ]
 
 
+class PrefillShape(ctypes.Structure):
+    _fields_ = [
+        ("tokens", c_uint32),
+        ("start", c_uint32),
+        ("query_heads", c_uint32),
+        ("kv_heads", c_uint32),
+        ("head_dim", c_uint32),
+        ("layers", c_uint32),
+        ("slots", c_uint32),
+        ("layer", c_uint32),
+        ("q_format", c_int32),
+        ("kv_format", c_int32),
+        ("scale", c_float),
+    ]
+
+
 _RECORDS = [c_void_p, c_void_p, c_uint32, c_void_p, c_uint64, c_uint32, c_void_p]
 SIGNATURES = {
     "lk_fp8_quantize": (c_int, _RECORDS),
@@ -53,6 +69,7 @@ SIGNATURES = {
     "lk_paged_decode_workspace": (c_uint64, [POINTER(DecodeShape)]),
     "lk_paged_decode": (c_int, [POINTER(DecodeShape), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint64, c_void_p]),
     "lk_stream_probe": (c_int, [c_void_p, c_void_p, c_uint64, c_void_p, c_void_p]),
+    "lk_paged_prefill": (c_int, [POINTER(PrefillShape), c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_void_p]),
     "lk_fp8_append": (c_int, [c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32,
                               c_uint32, c_uint32, c_void_p]),
 }

@@ -24,6 +24,23 @@ class BlockTable:
     num_tokens: int = 0
 
 
+@dataclass
+class PrefillChunk:
+    """Tokens [start, end) of one sequence as every layer of a prefill chunk sees them
+    (model.py:40-50): the ids of every block those tokens and the ones before them occupy,
+    and each chunk token's block and slot."""
+
+    start: int
+    end: int
+    block_ids: torch.Tensor
+    write_blocks: torch.Tensor
+    write_slots: torch.Tensor
+
+    @property
+    def tokens(self) -> int:
+        return self.end - self.start
+
+
 @dataclass(frozen=True)
 class DecodeBatch:
     write_blocks: torch.Tensor
@@ -49,6 +66,39 @@ class PagedKVCache:
 
     def blocks_for(self, tokens: int) -> int:
         return -(-tokens // self.block_tokens)
+
+    def _to_device(self, host: torch.Tensor) -> torch.Tensor:
+        """One copy to the device, from pinned memory so it queues behind launched work
+        (paged_cache.py:103-108)."""
+        if self.device.type != "cuda":
+            return host.to(self.device)
+        return host.pin_memory().to(self.device, non_blocking=True)
+
+    def chunk_locations(self, table: BlockTable, start: int, count: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """For tokens [start, start + count): the ids of every block they and the tokens before
+        them occupy (int32), then each token's block and slot (paged_cache.py:110-116)."""
+        if start < 0 or count < 1 or start + count > len(table.blocks) * self.block_tokens:
+            raise ValueError(f"tokens [{start}, {start + count}) do not fit a table of {len(table.blocks)} blocks")
+        ids = self._to_device(torch.tensor(table.blocks[: self.blocks_for(start + count)], dtype=torch.int32))
+        positions = torch.arange(start, start + count, device=self.device)
+        return ids, ids[positions // self.block_tokens].long(), positions % self.block_tokens
+
+    def chunk(self, table: BlockTable, start: int, count: int) -> PrefillChunk:
+        return PrefillChunk(start, start + count, *self.chunk_locations(table, start, count))
+
+    def write_at(self, blocks: torch.Tensor, slots: torch.Tensor, layer: int, k: torch.Tensor, v: torch.Tensor) -> None:
+        """Store k and v of shape [kv_heads, count, head_dim] at the given blocks and slots
+        (paged_cache.py:118-122)."""
+        self.pool[blocks, KEY, layer, :, slots] = k.transpose(0, 1).to(self.dtype)
+        self.pool[blocks, VALUE, layer, :, slots] = v.transpose(0, 1).to(self.dtype)
+
+    def read_blocks(self, ids: torch.Tensor, layer: int, end: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """K and V of the first `end` tokens held in blocks `ids`, as [kv_heads, end, head_dim]
+        (paged_cache.py:124-128): the gather the paged prefill kernel avoids."""
+        ids = ids.long()
+        k = self.pool[ids, KEY, layer].permute(1, 0, 2, 3).flatten(1, 2)[:, :end]
+        v = self.pool[ids, VALUE, layer].permute(1, 0, 2, 3).flatten(1, 2)[:, :end]
+        return k, v
 
     def decode_rows(self, tables: list[BlockTable], width: int | None = None) -> torch.Tensor:
         """int32 [batch, 3 + width]: write block, write slot, length, then the block table padded

@@ -171,6 +171,19 @@ def decode_attention(q: np.ndarray, pool_bits: np.ndarray, layer: int, table: np
     return out
 
 
+def prefill_attention(q: np.ndarray, pool_bits: np.ndarray, layer: int, block_ids, start: int, kv_groups: int) -> np.ndarray:
+    """Causal chunked prefill (model.py:69-98: query t of the chunk sees keys up to start + t),
+    composed from decode_attention above: query token t is one decode step of length
+    start + t + 1 over the same blocks. q [query_heads, tokens, dim] (float or BF16 bits);
+    returns float64 [query_heads, tokens, dim]."""
+    heads, tokens, dim = q.shape
+    table = np.asarray(block_ids, dtype=np.int32)[None]
+    out = np.zeros((heads, tokens, dim), dtype=np.float64)
+    for t in range(tokens):
+        out[:, t] = decode_attention(q[:, t][None], pool_bits, layer, table, np.array([start + t + 1]), kv_groups)[0]
+    return out
+
+
 def bf16_bits(values: np.ndarray) -> np.ndarray:
     """float32 -> BF16 bits, rounding to nearest even (NaN becomes 0x7FC0)."""
     wide = np.ascontiguousarray(values, dtype=np.float32).view(np.uint32).astype(np.uint64)

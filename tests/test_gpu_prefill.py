@@ -1,0 +1,131 @@
+"""Paged causal prefill (lk_paged_prefill) against the float64 oracle, through the C ABI.
+
+Tolerance: the north star's 2e-2 absolute / 1e-2 relative, plus a tighter check that the
+error stays within BF16 rounding of the output and of the weights (P enters the matrix cores
+as BF16): |err| <= 2^-7 |x| + 4e-3."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def make_pool(blocks, layers, kv_heads, seed, fp8=False):
+    from layover_amd.kernels.hip_decode import Fp8KVPool
+
+    rng = np.random.default_rng(seed)
+    bits = oracle.bf16_bits(rng.standard_normal((blocks, 2, layers, kv_heads, 16, 128), dtype=np.float32))
+    if not fp8:
+        return torch.from_numpy(bits.view(np.int16)).cuda().view(torch.bfloat16), bits
+    group_elems, groups = 16 * 128, 2 * layers * kv_heads
+    records = oracle.quantize_records(bits, list(range(blocks)), group_elems, groups)
+    state = np.zeros_like(bits)
+    oracle.dequantize_records(records, list(range(blocks)), state, group_elems, groups)
+    return Fp8KVPool(torch.from_numpy(records.reshape(blocks, -1)).cuda(), layers, kv_heads, 16, 128), state
+
+
+def assert_close(got, reference):
+    got = got.float().cpu().numpy().astype(np.float64)
+    err = np.abs(got - reference)
+    assert np.isfinite(got).all()
+    assert np.all(err <= 2e-2 + 1e-2 * np.abs(reference)), err.max()
+    assert np.all(err <= 2.0**-7 * np.abs(reference) + 4e-3), err.max()
+
+
+@pytest.mark.parametrize("start,tokens", [(0, 1), (0, 16), (0, 37), (5, 20), (16, 16), (100, 64), (1000, 130), (4090, 7)])
+def test_prefill_matches_the_oracle(start, tokens):
+    from layover_amd.kernels.hip_prefill import paged_prefill_attention_hip
+
+    end = start + tokens
+    blocks = -(-end // 16) + 3
+    pool, bits = make_pool(blocks, 3, 8, seed=start + tokens)
+    rng = np.random.default_rng(tokens)
+    block_ids = rng.permutation(blocks)[: -(-end // 16)].astype(np.int32)
+    q = torch.randn(32, tokens, 128, device="cuda").to(torch.bfloat16)
+    print(f"prefill start={start} tokens={tokens}", flush=True)
+    out = paged_prefill_attention_hip(q, pool, 1, torch.from_numpy(block_ids).cuda(), start, 4)
+    torch.cuda.synchronize()
+    assert_close(out, oracle.prefill_attention(q.float().cpu().numpy(), bits, 1, block_ids, start, 4))
+
+
+@pytest.mark.parametrize("query_heads", [8, 16, 40], ids=["gqa1", "gqa2", "gqa5"])
+def test_prefill_gqa_ratios(query_heads):
+    from layover_amd.kernels.hip_prefill import paged_prefill_attention_hip
+
+    pool, bits = make_pool(12, 2, 8, seed=query_heads)
+    block_ids = np.arange(11, -1, -1, dtype=np.int32)
+    q = torch.randn(query_heads, 45, 128, device="cuda").to(torch.bfloat16)
+    print(f"prefill gqa heads={query_heads}", flush=True)
+    out = paged_prefill_attention_hip(q, pool, 0, torch.from_numpy(block_ids).cuda(), 77, query_heads // 8)
+    torch.cuda.synchronize()
+    assert_close(out, oracle.prefill_attention(q.float().cpu().numpy(), bits, 0, block_ids, 77, query_heads // 8))
+
+
+@pytest.mark.parametrize("start,tokens", [(0, 24), (300, 90)])
+def test_prefill_reads_fp8_records(start, tokens):
+    from layover_amd.kernels.hip_prefill import paged_prefill_attention_hip
+
+    end = start + tokens
+    blocks = -(-end // 16)
+    pool, state = make_pool(blocks, 2, 8, seed=7, fp8=True)
+    block_ids = np.random.default_rng(8).permutation(blocks).astype(np.int32)
+    q = torch.randn(32, tokens, 128, device="cuda").to(torch.bfloat16)
+    print(f"prefill fp8 start={start} tokens={tokens}", flush=True)
+    out = paged_prefill_attention_hip(q, pool, 1, torch.from_numpy(block_ids).cuda(), start, 4)
+    torch.cuda.synchronize()
+    assert_close(out, oracle.prefill_attention(q.float().cpu().numpy(), state, 1, block_ids, start, 4))
+
+
+def test_slots_past_the_chunk_end_never_reach_the_output():
+    from layover_amd.kernels.hip_prefill import paged_prefill_attention_hip
+
+    pool, bits = make_pool(4, 1, 8, seed=11)
+    poisoned = bits.copy()
+    poisoned[3, :, 0, :, 9:] = 0x7FC0  # NaN in every slot of the last block past token 57
+    pool.copy_(torch.from_numpy(poisoned.view(np.int16)).cuda().view(torch.bfloat16))
+    block_ids = np.array([2, 0, 1, 3], dtype=np.int32)
+    q = torch.randn(32, 20, 128, device="cuda").to(torch.bfloat16)
+    out = paged_prefill_attention_hip(q, pool, 0, torch.from_numpy(block_ids).cuda(), 37, 4)
+    torch.cuda.synchronize()
+    assert_close(out, oracle.prefill_attention(q.float().cpu().numpy(), bits, 0, block_ids, 37, 4))
+
+
+def test_reference_signature_after_writing_the_chunk():
+    """cache.chunk + write_at + prefill_attention, as the reference's forward_prefill runs
+    them (model.py:131-135), for a first chunk and a later one."""
+    from layover_amd.config import ModelConfig
+    from layover_amd.kernels.hip_prefill import prefill_attention
+    from layover_amd.kv.paged_cache import BlockTable, PagedKVCache
+
+    cache = PagedKVCache(ModelConfig.qwen3_4b(), 20, device="cuda")
+    table = BlockTable(cache.allocator.alloc(9), 0)
+    for start, count in ((0, 70), (70, 61)):
+        chunk = cache.chunk(table, start, count)
+        k = torch.randn(8, count, 128, device="cuda").to(torch.bfloat16)
+        v = torch.randn(8, count, 128, device="cuda").to(torch.bfloat16)
+        q = torch.randn(32, count, 128, device="cuda").to(torch.bfloat16)
+        for layer in (0, 35):
+            cache.write_at(chunk.write_blocks, chunk.write_slots, layer, k, v)
+        out = prefill_attention(q, k, v, cache, 35, chunk, 4)
+        torch.cuda.synchronize()
+        bits = cache.pool.view(torch.int16).cpu().numpy().view(np.uint16)
+        assert_close(out, oracle.prefill_attention(q.float().cpu().numpy(), bits, 35, chunk.block_ids.cpu().numpy(), start, 4))
+
+
+def test_prefill_refuses_what_it_cannot_run():
+    from layover_amd.kernels.hip_prefill import paged_prefill_attention_hip
+
+    pool, _ = make_pool(3, 1, 8, seed=1)
+    q = torch.zeros(32, 10, 128, dtype=torch.bfloat16, device="cuda")
+    ids = torch.arange(3, dtype=torch.int32, device="cuda")
+    with pytest.raises(ValueError, match="blocks cannot hold"):
+        paged_prefill_attention_hip(q, pool, 0, ids[:1], 10, 4)
+    with pytest.raises(ValueError, match="KV heads"):
+        paged_prefill_attention_hip(q, pool, 0, ids, 0, 3)
+    with pytest.raises(ValueError, match="int32"):
+        paged_prefill_attention_hip(q, pool, 0, ids.long(), 0, 4)
+    with pytest.raises(ValueError, match="BF16"):
+        paged_prefill_attention_hip(q.float(), pool, 0, ids, 0, 4)
