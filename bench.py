@@ -15,6 +15,8 @@ Also measured in the same run (extra keys of the JSON line):
   decode_fp8  configs[3]: the same reading FP8 records, plus batch 1 @ 32,768 and 64 @ 4,096
   decode_graphs  small-batch decode steps (token write + attention, 36 layers) replayed as
               one HIP graph, against the same step launched eagerly; BF16 and FP8 pools
+  prefill     paged causal prefill of 2,048-token chunks at the start and at the end of a
+              32,768-token context, beside gather + torch flash attention on the same GPU
   overlap     configs[4]: decode steps while 2,048 blocks swap out and back in
   decode_distinct  configs[2] on a ~78 GB pool whose rows share no block
   hbm_probe   lk_stream_probe read and copy rates: the measured HBM ceiling
@@ -371,6 +373,61 @@ def graph_decode_bench(device, cache, fp8_pool, steps: int = 20) -> list:
 
 
 
+def prefill_bench(device, layers: int = 36) -> list:
+    """Paged causal prefill of one 2,048-token chunk (Qwen3-4B heads), per layer: the chunk
+    at the start of a sequence and at the end of a 32,768-token context. Beside it, the
+    reference's GPU path on this GPU (model.py:69-98): gather the history out of the pool,
+    then torch's flash attention with the bottom-right causal mask. FLOPs count the causal
+    score and value products: 4 x head_dim x visible keys per query row."""
+    import torch
+
+    from layover_amd.kernels.hip_prefill import paged_prefill_attention_hip
+
+    runs = []
+    for start, tokens in ((0, 2048), (30720, 2048)):
+        end = start + tokens
+        blocks = -(-end // 16)
+        pool = torch.empty(blocks + 1, 2, layers, QWEN["kv_heads"], 16, QWEN["head_dim"], dtype=torch.bfloat16, device=device)
+        fill_pool(pool, seed=13)
+        generator = torch.Generator(device=device).manual_seed(14)
+        ids = torch.randperm(blocks + 1, generator=generator, device=device)[:blocks].to(torch.int32)
+        q = torch.randn(QWEN["query_heads"], tokens, QWEN["head_dim"], generator=generator, device=device).to(torch.bfloat16)
+        groups = QWEN["query_heads"] // QWEN["kv_heads"]
+        flops = QWEN["query_heads"] * 4 * QWEN["head_dim"] * (tokens * start + tokens * (tokens + 1) // 2)
+
+        def ours(layer):
+            return paged_prefill_attention_hip(q, pool, layer, ids, start, groups)
+
+        def gathered(layer):
+            k = pool[ids.long(), 0, layer].permute(1, 0, 2, 3).flatten(1, 2)[:, :end].repeat_interleave(groups, 0)
+            v = pool[ids.long(), 1, layer].permute(1, 0, 2, 3).flatten(1, 2)[:, :end].repeat_interleave(groups, 0)
+            return torch.ops.aten._scaled_dot_product_flash_attention(q[None], k[None], v[None], 0.0, True)[0][0]
+
+        row = {"case": f"chunk_{tokens}_at_{start}"}
+        for name, fn in (("paged_prefill", ours), ("gather_then_torch_flash", gathered)):
+            try:
+                for layer in range(2):
+                    fn(layer)
+                torch.cuda.synchronize()
+                start_event, end_event = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                start_event.record()
+                for layer in range(layers):
+                    fn(layer)
+                end_event.record()
+                end_event.synchronize()
+                ms = start_event.elapsed_time(end_event) / layers
+                row[f"{name}_ms_per_layer"] = round(ms, 3)
+                row[f"{name}_tflops"] = round(flops / (ms * 1e-3) / 1e12, 1)
+            except Exception as error:  # torch's flash op may be absent from a build
+                row[f"{name}_error"] = repr(error)[:160]
+        row["frac_of_bf16_mfma_peak"] = round(row.get("paged_prefill_tflops", 0) / 2500.0, 4)
+        runs.append(row)
+        del pool
+        torch.cuda.empty_cache()
+    return runs
+
+
+
 def overlap_bench(device, cache, pool_blocks: int, swap_blocks: int = 2048) -> dict:
     """decode steps (batch 32, mixed contexts, BF16) on torch's stream
     while an FP8 swap of 2,048 blocks (32,768 tokens) runs on the backend's streams, then the
@@ -563,6 +620,7 @@ def main() -> None:
     parser.add_argument("--cpu-blocks", type=int, default=64)
     parser.add_argument("--skip-overlap", action="store_true")
     parser.add_argument("--skip-distinct", action="store_true")
+    parser.add_argument("--skip-graphs", action="store_true", help="skip the HIP-graph decode steps (rocprofv3 --pmc cannot follow replays)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this KV data path has no multi-GPU step (--gpus {args.gpus} refused)", file=sys.stderr)
@@ -666,11 +724,15 @@ def main() -> None:
             run = decode_bench(device, cache.pool, lengths, args.decode_steps, 1, seed=4, kv_pool=fp8_pool)
             fp8_runs.append({"case": name, **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in run.items()}})
         result["decode_fp8"] = fp8_runs
-        log("decode steps as HIP graph replays (batch 1 and 8)")
-        result["decode_graphs"] = graph_decode_bench(device, cache, fp8_pool)
+        if not args.skip_graphs:
+            log("decode steps as HIP graph replays (batch 1 and 8)")
+            result["decode_graphs"] = graph_decode_bench(device, cache, fp8_pool)
         del records, fp8_pool
         torch.cuda.empty_cache()
 
+    if not args.skip_decode:
+        log("paged prefill (2,048-token chunks)")
+        result["prefill"] = prefill_bench(device)
     if not args.skip_decode and not args.skip_overlap:
         log("overlap: decode during a 2,048-block FP8 swap (config 5)")
         result["overlap"] = overlap_bench(device, cache, pool_blocks)

@@ -32,17 +32,44 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float power_of_two(int32_t e) { return __uint_as_float(uint32_t(e + 127) << 23); }
 
-__device__ __forceinline__ void quantize_group(const uint16_t* __restrict__ pool, const int32_t* __restrict__ ids, uint8_t* __restrict__ stage,
-                                               uint32_t groups_per_block, uint64_t group, uint32_t lane) {
+// This wave's contiguous run of groups [first, stop) out of `total`: consecutive groups of a
+// block share its id, and a wave's next group is the next 4 KiB of the same block.
+__device__ __forceinline__ bool wave_range(uint64_t total, uint64_t& first, uint64_t& stop) {
+    const uint64_t waves = uint64_t(gridDim.x) * kCodecWaves;
+    // readfirstlane: the wave index is uniform, so group indices and block-id reads stay in
+    // scalar registers and scalar loads, whose waits do not wait on the vector loads in flight.
+    const uint64_t wave = uint64_t(blockIdx.x) * kCodecWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const uint64_t per = (total + waves - 1) / waves;
+    first = wave * per;
+    stop = first + per < total ? first + per : total;
+    return first < stop;
+}
+
+struct QuantizeLoad {
+    u32x4 words[4];
+    uint64_t group;
+};
+
+// The loads of one group: its 4 KiB of BF16, 4 x 16 bytes per lane.
+__device__ __forceinline__ void quantize_load(const uint16_t* __restrict__ pool, const int32_t* __restrict__ ids, uint32_t groups_per_block,
+                                              uint64_t group, uint32_t lane, QuantizeLoad& in) {
+    const uint32_t index = uint32_t(group / groups_per_block);
+    const uint32_t g = uint32_t(group % groups_per_block);
+    const uint64_t block_elems = uint64_t(kFastGroup) * groups_per_block;
+    const u32x4* source = reinterpret_cast<const u32x4*>(pool + uint64_t(ids[index]) * block_elems + uint64_t(g) * kFastGroup);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) in.words[j] = __builtin_nontemporal_load(source + j * kWave + lane);
+    in.group = group;
+}
+
+// Shift, codes and their stores for a loaded group.
+__device__ __forceinline__ void quantize_finish(uint8_t* __restrict__ stage, uint32_t groups_per_block, uint32_t lane, const QuantizeLoad& in) {
+    const uint64_t group = in.group;
     const uint32_t index = uint32_t(group / groups_per_block);
     const uint32_t g = uint32_t(group % groups_per_block);
     const uint64_t block_elems = uint64_t(kFastGroup) * groups_per_block;
     const uint64_t record = block_elems + 2ull * groups_per_block;
-    const u32x4* source = reinterpret_cast<const u32x4*>(pool + uint64_t(ids[index]) * block_elems + uint64_t(g) * kFastGroup);
-
-    u32x4 words[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) words[j] = __builtin_nontemporal_load(source + j * kWave + lane);
+    const u32x4* words = in.words;
 
     u16x2 keys = {0, 0};
     uint32_t flags = 0;
@@ -94,26 +121,58 @@ __global__ __launch_bounds__(kWave* kCodecWaves) void quantize_groups_2048(const
                                                                          const int32_t* __restrict__ ids, uint8_t* __restrict__ stage,
                                                                          uint32_t count, uint32_t groups_per_block) {
     const uint32_t lane = threadIdx.x % kWave;
-    const uint64_t total = uint64_t(count) * groups_per_block;
-    const uint64_t stride = uint64_t(gridDim.x) * kCodecWaves;
-    for (uint64_t group = uint64_t(blockIdx.x) * kCodecWaves + threadIdx.x / kWave; group < total; group += stride)
-        quantize_group(pool, ids, stage, groups_per_block, group, lane);
+    uint64_t group, stop;
+    if (!wave_range(uint64_t(count) * groups_per_block, group, stop)) return;
+    // Software-pipelined over two buffers that swap roles (no register copies, which would
+    // wait for the prefetched data): the next group's loads are in flight while one converts.
+    QuantizeLoad even, odd;
+    quantize_load(pool, ids, groups_per_block, group, lane, even);
+    while (true) {
+        if (group + 1 >= stop) {
+            quantize_finish(stage, groups_per_block, lane, even);
+            return;
+        }
+        quantize_load(pool, ids, groups_per_block, group + 1, lane, odd);
+        quantize_finish(stage, groups_per_block, lane, even);
+        if (++group + 1 >= stop) {
+            quantize_finish(stage, groups_per_block, lane, odd);
+            return;
+        }
+        quantize_load(pool, ids, groups_per_block, group + 1, lane, even);
+        quantize_finish(stage, groups_per_block, lane, odd);
+        ++group;
+    }
 }
 
-__device__ __forceinline__ void dequantize_group(const uint8_t* __restrict__ stage, const int32_t* __restrict__ ids, uint16_t* __restrict__ pool,
-                                                 uint32_t groups_per_block, uint64_t group, uint32_t lane) {
+struct DequantizeLoad {
+    u32x2 bytes[4];
+    int32_t shift;
+    int32_t block;
+    uint64_t group;
+};
+
+// The loads of one record group: 2 KiB of codes (4 x 8 bytes per lane), its shift, its block.
+__device__ __forceinline__ void dequantize_load(const uint8_t* __restrict__ stage, const int32_t* __restrict__ ids, uint32_t groups_per_block,
+                                                uint64_t group, uint32_t lane, DequantizeLoad& in) {
     const uint32_t index = uint32_t(group / groups_per_block);
     const uint32_t g = uint32_t(group % groups_per_block);
     const uint64_t block_elems = uint64_t(kFastGroup) * groups_per_block;
     const uint64_t record = block_elems + 2ull * groups_per_block;
-    const uint8_t* in = stage + uint64_t(index) * record;
-    const int32_t shift = *reinterpret_cast<const int16_t*>(in + block_elems + 2ull * g);
-    const u32x2* codes = reinterpret_cast<const u32x2*>(in + uint64_t(g) * kFastGroup);
-    u32x4* target = reinterpret_cast<u32x4*>(pool + uint64_t(ids[index]) * block_elems + uint64_t(g) * kFastGroup);
-
-    u32x2 bytes[4];
+    const uint8_t* base = stage + uint64_t(index) * record;
+    const u32x2* codes = reinterpret_cast<const u32x2*>(base + uint64_t(g) * kFastGroup);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) bytes[j] = __builtin_nontemporal_load(codes + j * kWave + lane);
+    for (int j = 0; j < 4; ++j) in.bytes[j] = __builtin_nontemporal_load(codes + j * kWave + lane);
+    in.shift = *reinterpret_cast<const int16_t*>(base + block_elems + 2ull * g);
+    in.block = ids[index];
+    in.group = group;
+}
+
+__device__ __forceinline__ void dequantize_finish(uint16_t* __restrict__ pool, uint32_t groups_per_block, uint32_t lane, const DequantizeLoad& in) {
+    const uint32_t g = uint32_t(in.group % groups_per_block);
+    const uint64_t block_elems = uint64_t(kFastGroup) * groups_per_block;
+    const int32_t shift = in.shift;
+    u32x4* target = reinterpret_cast<u32x4*>(pool + uint64_t(uint32_t(in.block)) * block_elems + uint64_t(g) * kFastGroup);
+    const u32x2* bytes = in.bytes;
 
     // A byte 0x7F or 0xFF (NaN) becomes 0x80 after masking off its sign and adding one.
     uint32_t flags = 0;
@@ -154,10 +213,25 @@ __global__ __launch_bounds__(kWave* kCodecWaves) void dequantize_groups_2048(con
                                                                            const int32_t* __restrict__ ids, uint16_t* __restrict__ pool,
                                                                            uint32_t count, uint32_t groups_per_block) {
     const uint32_t lane = threadIdx.x % kWave;
-    const uint64_t total = uint64_t(count) * groups_per_block;
-    const uint64_t stride = uint64_t(gridDim.x) * kCodecWaves;
-    for (uint64_t group = uint64_t(blockIdx.x) * kCodecWaves + threadIdx.x / kWave; group < total; group += stride)
-        dequantize_group(stage, ids, pool, groups_per_block, group, lane);
+    uint64_t group, stop;
+    if (!wave_range(uint64_t(count) * groups_per_block, group, stop)) return;
+    DequantizeLoad even, odd;
+    dequantize_load(stage, ids, groups_per_block, group, lane, even);
+    while (true) {
+        if (group + 1 >= stop) {
+            dequantize_finish(pool, groups_per_block, lane, even);
+            return;
+        }
+        dequantize_load(stage, ids, groups_per_block, group + 1, lane, odd);
+        dequantize_finish(pool, groups_per_block, lane, even);
+        if (++group + 1 >= stop) {
+            dequantize_finish(pool, groups_per_block, lane, odd);
+            return;
+        }
+        dequantize_load(stage, ids, groups_per_block, group + 1, lane, even);
+        dequantize_finish(pool, groups_per_block, lane, odd);
+        ++group;
+    }
 }
 
 void launch_quantize_2048(const uint16_t* pool, const int32_t* ids, uint8_t* stage, uint32_t count, uint32_t groups_per_block,

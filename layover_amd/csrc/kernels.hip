@@ -52,17 +52,15 @@ inline uint32_t grid_for_groups(uint64_t groups) {
     return uint32_t(workgroups);
 }
 
-// Persistent grid for the Qwen-shaped codec kernels: a few workgroups per CU, each wave
-// looping over groups. Once resident they keep their CU slots for the whole segment, which
-// matters when decode kernels on another stream fill the GPU (a grid of many short
-// workgroups has to win a dispatch slot every four groups). LAYOVER_CODEC_WG_PER_CU
-// overrides the count per CU (0: one workgroup per four groups, no loop). Measured on MI355X
-// (2,048-block swap-out during batch-32 decode): 111 ms with no loop, 79 ms at 16 per CU;
-// alone, the kernel's time per 113-block launch is unchanged within noise (63-66 us).
+// Grid of the Qwen-shaped codec kernels. By default one wave per group. LAYOVER_CODEC_WG_PER_CU
+// caps the grid at that many workgroups per CU instead, each wave then looping over a
+// contiguous run of groups with the next group's loads in flight. Measured on MI355X at the
+// bench's 113-block launches: alone, 63 us per launch uncapped against 66 us at 2-8 per CU;
+// a 2,048-block swap-out during batch-32 decode takes about 79 ms either way.
 uint32_t codec_grid(uint64_t groups) {
     static const uint32_t per_cu = [] {
         const char* text = getenv("LAYOVER_CODEC_WG_PER_CU");
-        return text ? uint32_t(strtoul(text, nullptr, 10)) : 16u;
+        return text ? uint32_t(strtoul(text, nullptr, 10)) : 0u;
     }();
     const uint32_t full = grid_for_groups(groups);
     if (per_cu == 0) return full;
