@@ -497,7 +497,15 @@ LK_EXPORT int lk_paged_prefill(const lk_prefill_shape* shape, const void* q, con
                     "q, out and pool blocks must be 16-byte aligned");
         const uint32_t groups = s.query_heads / s.kv_heads;
         const uint64_t rows = uint64_t(s.tokens) * groups;
-        const uint64_t row_tiles = (rows + lk::kPrefillRows * lk::kPrefillWaves - 1) / (lk::kPrefillRows * lk::kPrefillWaves);
+        // BF16 pools: the LDS-shared kernel (128 rows a workgroup) unless LAYOVER_PREFILL_KERNEL=1
+        // asks for the register-only one (64 rows), which also serves FP8-record pools.
+        static const bool register_only = [] {
+            const char* text = getenv("LAYOVER_PREFILL_KERNEL");
+            return text && strtoul(text, nullptr, 10) == 1;
+        }();
+        const bool shared = s.kv_format == LK_BF16 && !register_only;
+        const uint64_t tile_rows = shared ? uint64_t(lk::kLdsRows) * lk::kLdsWaves : uint64_t(lk::kPrefillRows) * lk::kPrefillWaves;
+        const uint64_t row_tiles = (rows + tile_rows - 1) / tile_rows;
         const uint64_t grid = row_tiles * s.kv_heads;
         lk::require(rows <= 0xFFFFFFFFull && grid <= 0x7FFFFFFFull, "prefill chunk too large for one launch");
         lk::PrefillArgs a{};
@@ -516,7 +524,9 @@ LK_EXPORT int lk_paged_prefill(const lk_prefill_shape* shape, const void* q, con
         a.block_bytes = block_bytes;
         a.scale_log2 = s.scale * lk::kLog2e;
         auto st = static_cast<hipStream_t>(stream);
-        if (s.kv_format == LK_BF16)
+        if (shared)
+            hipLaunchKernelGGL(lk::prefill_mfma_lds, dim3(uint32_t(grid)), dim3(lk::kWave * lk::kLdsWaves), 0, st, a);
+        else if (s.kv_format == LK_BF16)
             hipLaunchKernelGGL(lk::prefill_mfma<LK_BF16>, dim3(uint32_t(grid)), dim3(lk::kWave * lk::kPrefillWaves), 0, st, a);
         else
             hipLaunchKernelGGL(lk::prefill_mfma<LK_FP8_RECORD>, dim3(uint32_t(grid)), dim3(lk::kWave * lk::kPrefillWaves), 0, st, a);

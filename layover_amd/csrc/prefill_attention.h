@@ -261,6 +261,220 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_mfma(PrefillArgs
     }
 }
 
+// ---------------------------------------------------------------------------------------
+// BF16 pools: K/V shared through LDS. A workgroup of 4 waves owns 128 rows (32 per wave, as
+// two sets of 16) and walks the keys in steps of 32 (two blocks). Each step's K and V tiles
+// (4 x 4 KiB) are loaded once per workgroup, every thread bringing 64 contiguous bytes, into
+// one of two LDS buffers while the other is read; the next step's bytes are already in
+// registers, loaded one step ahead. Per wave and step:
+//   QK   for each block and set, four v_mfma_f32_16x16x32_bf16 on K read from LDS (lane
+//        (g, n): key n, dims 32g + 8j .. +8), reused by both sets;
+//   P    8 scores per lane (keys 4g..4g+3 of each block) of row n;
+//   PV   v_mfma_f32_16x16x32_bf16 over the step's 32 keys: the MFMA's k index 8g + i stands
+//        for key 4g + i of block 0 (i < 4) or of block 1 (i >= 4), in both P (the lane's
+//        own 8 weights, as BF16) and V (read from LDS as 16-byte rows of 8 dims, regrouped by
+//        v_perm per output dim), reused by both sets.
+// LDS rows are padded to 272 bytes so the 16 lanes reading one column of 16 rows hit
+// distinct banks.
+constexpr uint32_t kLdsWaves = 4;
+constexpr uint32_t kLdsRows = 32;                   // rows per wave
+constexpr uint32_t kLdsRowBytes = kDim * 2 + 16;    // 272
+constexpr uint32_t kLdsTile = kSlots * kLdsRowBytes; // one block's K or V
+constexpr uint32_t kLdsStep = 4 * kLdsTile;          // K0, K1, V0, V1
+
+__global__ __launch_bounds__(kWave* kLdsWaves) void prefill_mfma_lds(PrefillArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2][kLdsStep];
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const uint32_t g = lane / 16;
+    const uint32_t n = lane % 16;
+    const uint32_t kv_head = blockIdx.x % a.kv_heads;
+    const uint32_t tile = a.row_tiles - 1 - blockIdx.x / a.kv_heads;
+    const uint32_t total_rows = a.tokens * a.groups;
+    const uint32_t wg_row0 = tile * kLdsWaves * kLdsRows;
+    const uint32_t row0 = wg_row0 + wave * kLdsRows;
+    const uint32_t end = a.start + a.tokens;
+
+    // Keys the workgroup needs: up to its last row's limit; in steps of two blocks.
+    const uint32_t wg_last = min(wg_row0 + kLdsWaves * kLdsRows, total_rows) - 1;
+    const uint32_t key_blocks = (a.start + wg_last / a.groups) / kSlots + 1;
+    const uint32_t steps = (key_blocks + 1) / 2;
+    const uint32_t last_block = (end + kSlots - 1) / kSlots - 1;
+
+    // Per set: row n's token, head and causal limit; Q as the QK B operand.
+    int64_t limit[2];
+    uint32_t qt[2][16];
+#pragma unroll
+    for (int set = 0; set < 2; ++set) {
+        const uint32_t row = row0 + 16 * set + n;
+        const bool live = row < total_rows;
+        const uint32_t token = live ? row / a.groups : 0;
+        const uint32_t head = kv_head * a.groups + (live ? row % a.groups : 0);
+        limit[set] = live ? int64_t(a.start) + token : -1;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) qt[set][i] = 0;
+        if (live) {
+            const u32x4* src = reinterpret_cast<const u32x4*>(a.q + (uint64_t(head) * a.tokens + token) * kDim + 32 * g);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const u32x4 w = src[j];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) qt[set][4 * j + i] = w[i];
+            }
+        }
+    }
+
+    // Cooperative step loads: thread t brings 64 bytes of tile t / 64 (K0, K1, V0, V1).
+    const uint32_t part = threadIdx.x / kWave;          // which tile
+    const uint32_t piece = threadIdx.x % kWave;         // 64-byte piece of it
+    const uint64_t tile_bytes = uint64_t(kSlots) * kDim * 2;
+    const uint64_t head_tile = uint64_t(a.layer) * a.kv_heads + kv_head;
+    const uint64_t part_offset = (part < 2 ? head_tile : uint64_t(a.layers) * a.kv_heads + head_tile) * tile_bytes + uint64_t(piece) * 64;
+    const uint32_t lds_offset = part * kLdsTile + (piece / 4) * kLdsRowBytes + (piece % 4) * 64;
+    auto load_step = [&](uint32_t step, u32x4 (&r)[4]) {
+        const uint32_t block_index = min(2 * step + (part & 1), last_block);
+        const int32_t block = a.block_ids[block_index];
+        const u32x4* src = reinterpret_cast<const u32x4*>(a.pool + uint64_t(uint32_t(block)) * a.block_bytes + part_offset);
+#pragma unroll
+        for (int x = 0; x < 4; ++x) r[x] = src[x];
+    };
+    auto store_step = [&](uint32_t buffer, const u32x4 (&r)[4]) {
+        u32x4* dst = reinterpret_cast<u32x4*>(lds[buffer] + lds_offset);
+#pragma unroll
+        for (int x = 0; x < 4; ++x) dst[x] = r[x];
+    };
+
+    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
+    f32x4 o[2][8];
+#pragma unroll
+    for (int set = 0; set < 2; ++set)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[set][e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    u32x4 staged[4];
+    load_step(0, staged);
+    store_step(0, staged);
+    if (steps > 1) load_step(1, staged);
+    __syncthreads();
+
+    for (uint32_t step = 0; step < steps; ++step) {
+        const uint8_t* buf = lds[step & 1];
+        const uint32_t key0 = step * 2 * kSlots;
+
+        // Scores S^T = K Q^T for both blocks and both sets.
+        f32x4 s[2][2];
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            const uint8_t* k_row = buf + b * kLdsTile + n * kLdsRowBytes + 64 * g;
+            bf16x8 kk[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) kk[j] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(k_row + 16 * j));
+#pragma unroll
+            for (int set = 0; set < 2; ++set) {
+                f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        kk[j], as_bf16x8(qt[set][4 * j], qt[set][4 * j + 1], qt[set][4 * j + 2], qt[set][4 * j + 3]), acc, 0, 0, 0);
+                s[set][b] = acc;
+            }
+        }
+
+        // V of the step as B operands: for output dim 8n + e, the values of keys
+        // (4g + r of block 0, then of block 1), as four BF16 pairs.
+        u32x4 rows[2][4];
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                rows[b][r] = *reinterpret_cast<const u32x4*>(buf + (2 + b) * kLdsTile + (4 * g + r) * kLdsRowBytes + 16 * n);
+        // Keys at or past the chunk's end hold anything: zero their V (0 * NaN is NaN).
+        if (key0 + 2 * kSlots > end) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (key0 + b * kSlots + 4 * g + r >= end) rows[b][r] = u32x4{0u, 0u, 0u, 0u};
+        }
+
+#pragma unroll
+        for (int set = 0; set < 2; ++set) {
+            float score[8];
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int64_t key = int64_t(key0 + b * kSlots + 4 * g + r);
+                    score[4 * b + r] = key <= limit[set] ? s[set][b][r] * a.scale_log2 : -INFINITY;
+                }
+            float top = score[0];
+#pragma unroll
+            for (int i = 1; i < 8; ++i) top = fmaxf(top, score[i]);
+            top = fmaxf(top, __shfl_xor(top, 16, kWave));
+            top = fmaxf(top, __shfl_xor(top, 32, kWave));
+            if (__builtin_expect(__any(top > m[set] + kRescaleThreshold), 0)) {
+                asm volatile("" ::: "memory");
+                const float next = top > m[set] + kRescaleThreshold ? top : m[set];
+                const float alpha = merge_weight(m[set], next);
+                m[set] = next;
+                l[set] *= alpha;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float factor = __shfl(alpha, int(4 * g + r), kWave);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) o[set][e][r] *= factor;
+                }
+            }
+            float p[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                p[i] = score[i] == -INFINITY ? 0.0f : exp2_fast(score[i] - m[set]);
+                l[set] += p[i];
+            }
+            const bf16x8 pb = as_bf16x8(pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]), pack_bf16(p[4], p[5]), pack_bf16(p[6], p[7]));
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t select = (e & 1) ? 0x07060302u : 0x05040100u;
+                const uint32_t w = e / 2;
+                const bf16x8 vb = as_bf16x8(__builtin_amdgcn_perm(rows[0][1][w], rows[0][0][w], select),
+                                            __builtin_amdgcn_perm(rows[0][3][w], rows[0][2][w], select),
+                                            __builtin_amdgcn_perm(rows[1][1][w], rows[1][0][w], select),
+                                            __builtin_amdgcn_perm(rows[1][3][w], rows[1][2][w], select));
+                o[set][e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pb, vb, o[set][e], 0, 0, 0);
+            }
+        }
+
+        // The next step's tiles into the other buffer; then the one after into registers.
+        if (step + 1 < steps) {
+            store_step((step + 1) & 1, staged);
+            if (step + 2 < steps) load_step(step + 2, staged);
+        }
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int set = 0; set < 2; ++set) {
+        float total = l[set];
+        total += __shfl_xor(total, 16, kWave);
+        total += __shfl_xor(total, 32, kWave);
+        const float inverse = 1.0f / total;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float factor = __shfl(inverse, int(4 * g + r), kWave);
+            const uint32_t out_row = row0 + 16 * set + 4 * g + r;
+            if (out_row < total_rows) {
+                const uint32_t out_token = out_row / a.groups;
+                const uint32_t out_head = kv_head * a.groups + out_row % a.groups;
+                u32x4 packed;
+#pragma unroll
+                for (int x = 0; x < 4; ++x)
+                    packed[x] = uint32_t(to_bf16(o[set][2 * x][r] * factor)) | (uint32_t(to_bf16(o[set][2 * x + 1][r] * factor)) << 16);
+                *reinterpret_cast<u32x4*>(a.out + (uint64_t(out_head) * a.tokens + out_token) * kDim + 8 * n) = packed;
+            }
+        }
+    }
+}
+
 }  // namespace lk
 
 #endif  // LAYOVER_AMD_PREFILL_ATTENTION_H
