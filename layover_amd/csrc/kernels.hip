@@ -497,13 +497,11 @@ LK_EXPORT int lk_paged_prefill(const lk_prefill_shape* shape, const void* q, con
                     "q, out and pool blocks must be 16-byte aligned");
         const uint32_t groups = s.query_heads / s.kv_heads;
         const uint64_t rows = uint64_t(s.tokens) * groups;
-        // BF16 pools: the LDS-shared kernel (128 rows a workgroup) unless LAYOVER_PREFILL_KERNEL=1
-        // asks for the register-only one (64 rows), which also serves FP8-record pools.
-        static const bool register_only = [] {
-            const char* text = getenv("LAYOVER_PREFILL_KERNEL");
-            return text && strtoul(text, nullptr, 10) == 1;
-        }();
-        const bool shared = s.kv_format == LK_BF16 && !register_only;
+        // The LDS-shared kernel (128 rows a workgroup) unless LAYOVER_PREFILL_KERNEL=1 asks for
+        // the register-only one (64 rows a workgroup, each wave streaming its own tiles).
+        const char* choice = getenv("LAYOVER_PREFILL_KERNEL");
+        const bool register_only = choice && strtoul(choice, nullptr, 10) == 1;
+        const bool shared = !register_only;
         const uint64_t tile_rows = shared ? uint64_t(lk::kLdsRows) * lk::kLdsWaves : uint64_t(lk::kPrefillRows) * lk::kPrefillWaves;
         const uint64_t row_tiles = (rows + tile_rows - 1) / tile_rows;
         const uint64_t grid = row_tiles * s.kv_heads;
@@ -524,8 +522,10 @@ LK_EXPORT int lk_paged_prefill(const lk_prefill_shape* shape, const void* q, con
         a.block_bytes = block_bytes;
         a.scale_log2 = s.scale * lk::kLog2e;
         auto st = static_cast<hipStream_t>(stream);
-        if (shared)
-            hipLaunchKernelGGL(lk::prefill_mfma_lds, dim3(uint32_t(grid)), dim3(lk::kWave * lk::kLdsWaves), 0, st, a);
+        if (shared && s.kv_format == LK_BF16)
+            hipLaunchKernelGGL(lk::prefill_mfma_lds<LK_BF16>, dim3(uint32_t(grid)), dim3(lk::kWave * lk::kLdsWaves), 0, st, a);
+        else if (shared)
+            hipLaunchKernelGGL(lk::prefill_mfma_lds<LK_FP8_RECORD>, dim3(uint32_t(grid)), dim3(lk::kWave * lk::kLdsWaves), 0, st, a);
         else if (s.kv_format == LK_BF16)
             hipLaunchKernelGGL(lk::prefill_mfma<LK_BF16>, dim3(uint32_t(grid)), dim3(lk::kWave * lk::kPrefillWaves), 0, st, a);
         else

@@ -285,8 +285,20 @@ constexpr uint32_t kLdsRowBytes = kDim * 2 + 16;    // 272
 constexpr uint32_t kLdsTile = kSlots * kLdsRowBytes; // one block's K or V
 constexpr uint32_t kLdsStep = 4 * kLdsTile;          // K0, K1, V0, V1
 
+// FP8-record pools: each thread converts its 32 codes to BF16 as it stages them (the exact
+// hardware convert), and each block's 2^shift is applied to that block's scores (K) and
+// weights (V), one factor per block and step kept beside the tiles in LDS. A block whose shift
+// could leave BF16's normal range is decoded exactly with the shift included (the reference's
+// decode_bits) and gets factor 1.
+struct PrefillStaged {
+    u32x4 w[4];  // BF16: 64 bytes; FP8: the first two hold 32 codes
+    int32_t shift;
+};
+
+template <int KV>
 __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_mfma_lds(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[2][kLdsStep];
+    __shared__ int32_t lds_shift[2][4];  // FP8: per buffer, the shift of K0, K1, V0, V1
     const uint32_t lane = threadIdx.x % kWave;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const uint32_t g = lane / 16;
@@ -327,24 +339,46 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
         }
     }
 
-    // Cooperative step loads: thread t brings 64 bytes of tile t / 64 (K0, K1, V0, V1).
+    // Cooperative step loads: thread t brings piece t % 64 of tile t / 64 (K0, K1, V0, V1):
+    // 64 bytes of BF16, or 32 FP8 codes that become 64 bytes of BF16 in LDS.
+    constexpr uint32_t kElem = KV == LK_FP8_RECORD ? 1 : 2;
     const uint32_t part = threadIdx.x / kWave;          // which tile
-    const uint32_t piece = threadIdx.x % kWave;         // 64-byte piece of it
-    const uint64_t tile_bytes = uint64_t(kSlots) * kDim * 2;
+    const uint32_t piece = threadIdx.x % kWave;         // which 32 values of it
+    const uint64_t tile_bytes = uint64_t(kSlots) * kDim * kElem;
     const uint64_t head_tile = uint64_t(a.layer) * a.kv_heads + kv_head;
-    const uint64_t part_offset = (part < 2 ? head_tile : uint64_t(a.layers) * a.kv_heads + head_tile) * tile_bytes + uint64_t(piece) * 64;
+    const uint64_t group = part < 2 ? head_tile : uint64_t(a.layers) * a.kv_heads + head_tile;
+    const uint64_t part_offset = group * tile_bytes + uint64_t(piece) * 32 * kElem;
+    const uint64_t block_elems = uint64_t(2) * a.layers * a.kv_heads * kSlots * kDim;
     const uint32_t lds_offset = part * kLdsTile + (piece / 4) * kLdsRowBytes + (piece % 4) * 64;
-    auto load_step = [&](uint32_t step, u32x4 (&r)[4]) {
+    auto load_step = [&](uint32_t step, PrefillStaged& r) {
         const uint32_t block_index = min(2 * step + (part & 1), last_block);
         const int32_t block = a.block_ids[block_index];
-        const u32x4* src = reinterpret_cast<const u32x4*>(a.pool + uint64_t(uint32_t(block)) * a.block_bytes + part_offset);
+        const uint8_t* base = a.pool + uint64_t(uint32_t(block)) * a.block_bytes;
+        const u32x4* src = reinterpret_cast<const u32x4*>(base + part_offset);
+        if constexpr (KV == LK_BF16) {
 #pragma unroll
-        for (int x = 0; x < 4; ++x) r[x] = src[x];
+            for (int x = 0; x < 4; ++x) r.w[x] = src[x];
+        } else {
+            r.w[0] = src[0];
+            r.w[1] = src[1];
+            r.shift = reinterpret_cast<const int16_t*>(base + block_elems)[group];
+        }
     };
-    auto store_step = [&](uint32_t buffer, const u32x4 (&r)[4]) {
+    auto store_step = [&](uint32_t buffer, const PrefillStaged& r) {
         u32x4* dst = reinterpret_cast<u32x4*>(lds[buffer] + lds_offset);
+        if constexpr (KV == LK_BF16) {
 #pragma unroll
-        for (int x = 0; x < 4; ++x) dst[x] = r[x];
+            for (int x = 0; x < 4; ++x) dst[x] = r.w[x];
+        } else {
+            const bool exact = !shift_is_exact_in_fp32(r.shift);
+#pragma unroll
+            for (int x = 0; x < 4; ++x) {
+                const uint32_t lo = r.w[x / 2][2 * (x % 2)], hi = r.w[x / 2][2 * (x % 2) + 1];
+                dst[x] = u32x4{fp8_pair(lo, false, exact, r.shift), fp8_pair(lo, true, exact, r.shift), fp8_pair(hi, false, exact, r.shift),
+                               fp8_pair(hi, true, exact, r.shift)};
+            }
+            if (piece == 0) lds_shift[buffer][part] = r.shift;
+        }
     };
 
     float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
@@ -354,7 +388,7 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[set][e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    u32x4 staged[4];
+    PrefillStaged staged;
     load_step(0, staged);
     store_step(0, staged);
     if (steps > 1) load_step(1, staged);
@@ -363,6 +397,15 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
     for (uint32_t step = 0; step < steps; ++step) {
         const uint8_t* buf = lds[step & 1];
         const uint32_t key0 = step * 2 * kSlots;
+        float k_factor[2] = {a.scale_log2, a.scale_log2}, v_factor[2] = {1.0f, 1.0f};
+        if constexpr (KV == LK_FP8_RECORD) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+                const int32_t ks = lds_shift[step & 1][b], vs = lds_shift[step & 1][2 + b];
+                if (shift_is_exact_in_fp32(ks)) k_factor[b] *= pow2(ks);
+                if (shift_is_exact_in_fp32(vs)) v_factor[b] = pow2(vs);
+            }
+        }
 
         // Scores S^T = K Q^T for both blocks and both sets.
         f32x4 s[2][2];
@@ -408,7 +451,7 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int64_t key = int64_t(key0 + b * kSlots + 4 * g + r);
-                    score[4 * b + r] = key <= limit[set] ? s[set][b][r] * a.scale_log2 : -INFINITY;
+                    score[4 * b + r] = key <= limit[set] ? s[set][b][r] * k_factor[b] : -INFINITY;
                 }
             float top = score[0];
 #pragma unroll
@@ -433,6 +476,7 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
             for (int i = 0; i < 8; ++i) {
                 p[i] = score[i] == -INFINITY ? 0.0f : exp2_fast(score[i] - m[set]);
                 l[set] += p[i];
+                p[i] *= v_factor[i / 4];
             }
             const bf16x8 pb = as_bf16x8(pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]), pack_bf16(p[4], p[5]), pack_bf16(p[6], p[7]));
 #pragma unroll

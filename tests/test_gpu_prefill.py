@@ -129,3 +129,35 @@ def test_prefill_refuses_what_it_cannot_run():
         paged_prefill_attention_hip(q, pool, 0, ids.long(), 0, 4)
     with pytest.raises(ValueError, match="BF16"):
         paged_prefill_attention_hip(q.float(), pool, 0, ids, 0, 4)
+
+
+@pytest.mark.parametrize("kernel", ["lds", "register_only"])
+def test_prefill_fp8_tiny_groups_take_the_exact_decode(kernel, monkeypatch):
+    """Groups scaled by 2^-114 get shifts below -117, where the hardware convert times
+    2^shift could leave BF16's normal range; those blocks are decoded with the reference's
+    integer decode instead. Every V group and the K groups of half the blocks are scaled, and
+    the output (about 2^-114 in size) is compared after scaling back by 2^114."""
+    from layover_amd.kernels.hip_decode import Fp8KVPool
+    from layover_amd.kernels.hip_prefill import paged_prefill_attention_hip
+
+    monkeypatch.setenv("LAYOVER_PREFILL_KERNEL", "1" if kernel == "register_only" else "0")
+    blocks, layers = 8, 2
+    rng = np.random.default_rng(21)
+    values = rng.standard_normal((blocks, 2, layers, 8, 16, 128), dtype=np.float32)
+    values[::2, 0] *= np.float32(2.0**-114)
+    values[:, 1] *= np.float32(2.0**-114)
+    bits = oracle.bf16_bits(values)
+    group_elems, groups = 16 * 128, 2 * layers * 8
+    records = oracle.quantize_records(bits, list(range(blocks)), group_elems, groups)
+    shifts = records.reshape(blocks, -1)[:, group_elems * groups :].copy().view(np.int16)
+    assert (shifts < -117).sum() >= blocks * layers * 8 * 3 // 2
+    state = np.zeros_like(bits)
+    oracle.dequantize_records(records, list(range(blocks)), state, group_elems, groups)
+    pool = Fp8KVPool(torch.from_numpy(records.reshape(blocks, -1)).cuda(), layers, 8, 16, 128)
+    block_ids = np.array([3, 0, 6, 1, 4, 7, 2, 5], dtype=np.int32)
+    q = torch.randn(32, 60, 128, device="cuda").to(torch.bfloat16)
+    print(f"prefill fp8 exact decode, {kernel}", flush=True)
+    out = paged_prefill_attention_hip(q, pool, 1, torch.from_numpy(block_ids).cuda(), 50, 4)
+    torch.cuda.synchronize()
+    reference = oracle.prefill_attention(q.float().cpu().numpy(), state, 1, block_ids, 50, 4)
+    assert_close(out.float() * 2.0**114, reference * 2.0**114)
