@@ -421,8 +421,28 @@ def prefill_bench(device, layers: int = 36) -> list:
             except Exception as error:  # torch's flash op may be absent from a build
                 row[f"{name}_error"] = repr(error)[:160]
         row["frac_of_bf16_mfma_peak"] = round(row.get("paged_prefill_tflops", 0) / 2500.0, 4)
+        # The same chunk over an FP8-resident copy of the pool.
+        from layover_amd.kernels.fp8 import Fp8Layout, quantize_blocks
+        from layover_amd.kernels.hip_decode import Fp8KVPool
+
+        layout = Fp8Layout.for_pool(pool)
+        records = torch.empty(pool.shape[0], layout.record_bytes, dtype=torch.uint8, device=device)
+        quantize_blocks(pool, torch.arange(pool.shape[0], dtype=torch.int32, device=device), records.view(-1), layout)
+        fp8_pool = Fp8KVPool(records, layers, QWEN["kv_heads"], 16, QWEN["head_dim"])
+        for layer in range(2):
+            paged_prefill_attention_hip(q, fp8_pool, layer, ids, start, groups)
+        torch.cuda.synchronize()
+        start_event, end_event = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start_event.record()
+        for layer in range(layers):
+            paged_prefill_attention_hip(q, fp8_pool, layer, ids, start, groups)
+        end_event.record()
+        end_event.synchronize()
+        ms = start_event.elapsed_time(end_event) / layers
+        row["paged_prefill_fp8_pool_ms_per_layer"] = round(ms, 3)
+        row["paged_prefill_fp8_pool_tflops"] = round(flops / (ms * 1e-3) / 1e12, 1)
         runs.append(row)
-        del pool
+        del pool, records, fp8_pool
         torch.cuda.empty_cache()
     return runs
 
