@@ -12,6 +12,7 @@
  *                      reference counterpart (the reference decodes BF16 and FP32 pools only).
  *   lk_paged_prefill   layover/model.py:69-98 prefill_attention (gather + FlashAttention),
  *                      read in place instead of gathered.
+ *   lk_kv_write        layover/model.py:139-140, the decode-time pool write, as one kernel.
  *   lk_fp8_append      no counterpart: the FP8-resident pool's version of the decode-time
  *                      pool write of layover/model.py:139-140.
  *
@@ -124,6 +125,15 @@ typedef struct {
 
 int lk_paged_prefill(const lk_prefill_shape* shape, const void* q, const void* pool, const int32_t* block_ids, uint32_t num_block_ids,
                      void* out, void* stream);
+
+/* One decode step's KV write into a BF16 pool, the reference's indexed assignment
+ * (layover/model.py:139-140) as one launch: for row b, slot write_slot[b*row_stride] of block
+ * write_block[b*row_stride], layer `layer`, takes k[b] (K) and v[b] (V), BF16 [batch,
+ * kv_heads, head_dim] contiguous. head_dim a multiple of 8; pool, k and v 16-byte aligned.
+ * Ids and slots are not checked. */
+int lk_kv_write(void* pool, const int32_t* write_block, const int32_t* write_slot, uint32_t row_stride, uint32_t batch,
+                const void* k, const void* v, uint32_t layer, uint32_t layers, uint32_t kv_heads, uint32_t slots,
+                uint32_t head_dim, void* stream);
 
 /* One decode step's KV write into an FP8-record pool: no reference counterpart (the
  * reference writes BF16 tokens into a BF16 pool, layover/model.py:139-140). For row b,

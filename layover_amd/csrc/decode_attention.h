@@ -210,11 +210,15 @@ __global__ __launch_bounds__(kWave* kDecodeWaves) void decode_split_mfma(DecodeA
     if (!decode_unit_of(a, blockIdx.x, &seq, &split, &kv_head)) return;
     const uint32_t groups = a.groups;
 
-    const int32_t length = a.lengths[uint64_t(seq) * a.lengths_stride];
-    const uint32_t nblocks = blocks_of(length, kSlots);
+    // The split's block ids are loaded (one per lane, this wave's units) before the length
+    // is known, bounded by the table width alone, so the two loads overlap; the length then
+    // decides how many are used.
     const uint32_t first = split * a.bps;
-    if (first >= nblocks) return;
-    const uint32_t count = min(a.bps, nblocks - first);
+    const int32_t* row_ids = a.table + uint64_t(seq) * a.table_stride + first;
+    const uint32_t width_here = min(a.bps, a.table_width - first);
+    const uint32_t listed = width_here > wave ? (width_here - wave + kDecodeWaves - 1) / kDecodeWaves : 0;
+    const int32_t listed_block = lane < listed ? row_ids[wave + lane * kDecodeWaves] : 0;
+    const int32_t length = a.lengths[uint64_t(seq) * a.lengths_stride];
 
     // B operands of QK: query head n (zero past the group), dims 32g + 8j .. +8 for step j.
     // An FP32 q is split into BF16 hi + lo parts, one MFMA each.
@@ -248,19 +252,23 @@ __global__ __launch_bounds__(kWave* kDecodeWaves) void decode_split_mfma(DecodeA
         }
     }
 
+    // q, the ids and the length are in flight together; only now is the length needed.
+    const uint32_t nblocks = blocks_of(length, kSlots);
+    if (first >= nblocks) return;
+    const uint32_t count = min(a.bps, nblocks - first);
+
     constexpr uint32_t kElem = KV == LK_FP8_RECORD ? 1 : 2;
     const uint64_t tile_bytes = uint64_t(kSlots) * kDim * kElem;
     const uint64_t head_tile = uint64_t(a.layer) * a.kv_heads + kv_head;  // group index of K
     const uint64_t k_offset = head_tile * tile_bytes + (uint64_t(n) * kDim + 32 * g) * kElem;
     const uint64_t v_offset = (uint64_t(a.layers) * a.kv_heads + head_tile) * tile_bytes + (uint64_t(4 * g) * kDim + 8 * n) * kElem;
     const uint64_t block_elems = uint64_t(2) * a.layers * a.kv_heads * kSlots * kDim;  // FP8: shifts follow the data
-    const int32_t* row_ids = a.table + uint64_t(seq) * a.table_stride + first;
 
     // The block ids (and FP8 shifts) of this wave's units, one unit per lane (at most 64:
-    // blocks per split <= 256), loaded before any tile and read back with v_readlane, so no
-    // load inside the main loop has to wait for the tile loads issued ahead of it.
+    // blocks per split <= 256), held before any tile is loaded and read back with v_readlane,
+    // so no load inside the main loop has to wait for the tile loads issued ahead of it.
     const uint32_t mine = count > wave ? (count - wave + kDecodeWaves - 1) / kDecodeWaves : 0;
-    const int32_t my_block = lane < mine ? row_ids[wave + lane * kDecodeWaves] : 0;
+    const int32_t my_block = lane < mine ? listed_block : 0;
     int32_t my_k_shift = 0, my_v_shift = 0;
     if constexpr (KV == LK_FP8_RECORD) {
         if (lane < mine) {

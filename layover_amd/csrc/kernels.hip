@@ -333,6 +333,31 @@ __global__ __launch_bounds__(kWave* kCodecWaves) void append_groups_2048(uint8_t
     if (lane == 0) *shift_at = int16_t(shift);
 }
 
+
+// One token per sequence written into a BF16 pool (lk_kv_write): the reference's decode-time
+// pool assignment (model.py:139-140) as one launch. Thread t of a row copies 16 bytes: K for
+// the first kv_heads * head_dim / 8 threads, V for the rest.
+__global__ void write_tokens_bf16(uint16_t* __restrict__ pool, const int32_t* __restrict__ write_block,
+                                  const int32_t* __restrict__ write_slot, uint32_t row_stride, uint32_t batch,
+                                  const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, uint32_t layer, uint32_t layers,
+                                  uint32_t kv_heads, uint32_t slots, uint32_t head_dim) {
+    const uint32_t per_kind = kv_heads * head_dim / 8;  // 16-byte pieces of one kind
+    const uint64_t index = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (index >= uint64_t(batch) * 2 * per_kind) return;
+    const uint32_t row = uint32_t(index / (2 * per_kind));
+    const uint32_t within = uint32_t(index % (2 * per_kind));
+    const uint32_t kind = within / per_kind;
+    const uint32_t piece = within % per_kind;
+    const uint32_t head = piece * 8 / head_dim;
+    const uint32_t dim = piece * 8 % head_dim;
+    const uint64_t block = uint32_t(write_block[uint64_t(row) * row_stride]);
+    const uint64_t slot = uint32_t(write_slot[uint64_t(row) * row_stride]);
+    const uint64_t tile = ((uint64_t(kind) * layers + layer) * kv_heads + head) * slots + slot;
+    const uint64_t block_elems = 2ull * layers * kv_heads * slots * head_dim;
+    const u32x4 value = *reinterpret_cast<const u32x4*>((kind == 0 ? k : v) + (uint64_t(row) * kv_heads + head) * head_dim + dim);
+    *reinterpret_cast<u32x4*>(pool + block * block_elems + tile * head_dim + dim) = value;
+}
+
 }  // namespace lk
 
 #define LK_EXPORT extern "C" __attribute__((visibility("default")))
@@ -393,6 +418,26 @@ LK_EXPORT int lk_fp8_decode(const uint8_t* codes, uint16_t* out, uint64_t n, int
         const uint64_t grid = (n + 255) / 256;
         lk::require(grid <= 0x7FFFFFFFull, "too many elements for one launch");
         hipLaunchKernelGGL(lk::decode_elements, dim3(uint32_t(grid)), dim3(256), 0, static_cast<hipStream_t>(stream), codes, out, n, shift);
+    });
+}
+
+LK_EXPORT int lk_kv_write(void* pool, const int32_t* write_block, const int32_t* write_slot, uint32_t row_stride, uint32_t batch,
+                          const void* k, const void* v, uint32_t layer, uint32_t layers, uint32_t kv_heads, uint32_t slots,
+                          uint32_t head_dim, void* stream) {
+    return lk::guarded([&] {
+        lk::require(pool && write_block && write_slot && k && v, "null pool, write rows, k or v");
+        lk::require(layers > 0 && kv_heads > 0 && slots > 0 && head_dim > 0, "every pool dimension must be positive");
+        lk::require(layer < layers, "layer out of range");
+        lk::require(row_stride > 0, "row_stride must be positive");
+        lk::require(head_dim % 8 == 0 && lk::aligned(pool, 16) && lk::aligned(k, 16) && lk::aligned(v, 16),
+                    "head_dim must be a multiple of 8 and pool, k and v 16-byte aligned");
+        if (batch == 0) return;
+        const uint64_t threads = uint64_t(batch) * 2 * kv_heads * head_dim / 8;
+        const uint64_t grid = (threads + 255) / 256;
+        lk::require(grid <= 0x7FFFFFFFull, "too many rows for one launch");
+        hipLaunchKernelGGL(lk::write_tokens_bf16, dim3(uint32_t(grid)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                           static_cast<uint16_t*>(pool), write_block, write_slot, row_stride, batch, static_cast<const uint16_t*>(k),
+                           static_cast<const uint16_t*>(v), layer, layers, kv_heads, slots, head_dim);
     });
 }
 

@@ -70,21 +70,7 @@ class Fp8KVPool:
         not checked against the pool: the caller has (as decode_rows does). Rows must name
         distinct (block, layer) groups; two rows writing one group race. Enqueued on the
         current stream."""
-        if not 0 <= layer < self.layers:
-            raise ValueError(f"layer {layer} out of range for {self.layers} layers")
-        batch = write_blocks.shape[0]
-        for name, rows in (("write_blocks", write_blocks), ("write_slots", write_slots)):
-            if rows.dtype != torch.int32 or rows.dim() != 1 or rows.shape[0] != batch:
-                raise ValueError(f"{name} must be 1-D int32 with one entry per row")
-        if batch and write_blocks.stride(0) != write_slots.stride(0):
-            raise ValueError("write_blocks and write_slots must share one row stride")
-        expected = (batch, self.kv_heads, self.head_dim)
-        for name, t in (("k", k), ("v", v)):
-            if t.dtype != torch.bfloat16 or tuple(t.shape) != expected or not t.is_contiguous():
-                raise ValueError(f"{name} must be contiguous BF16 shaped {expected}")
-        devices = {self.records.device, write_blocks.device, write_slots.device, k.device, v.device}
-        if len(devices) != 1 or self.records.device.type != "cuda":
-            raise ValueError("the pool, rows, k and v must be on one GPU")
+        batch = _check_token_write(self.records.device, self.layers, self.kv_heads, self.head_dim, write_blocks, write_slots, layer, k, v)
         if batch == 0:
             return
         _lib.check(
@@ -97,6 +83,45 @@ class Fp8KVPool:
     def empty(cls, blocks: int, layers: int, kv_heads: int, slots: int, head_dim: int, device) -> "Fp8KVPool":
         layout = Fp8Layout(slots * head_dim, KV_KINDS * layers * kv_heads)
         return cls(torch.zeros(blocks, layout.record_bytes, dtype=torch.uint8, device=device), layers, kv_heads, slots, head_dim)
+
+
+def _check_token_write(device, layers, kv_heads, head_dim, write_blocks, write_slots, layer, k, v) -> int:
+    """Arguments of a decode-time token write, from tensor metadata alone; returns the rows."""
+    if not 0 <= layer < layers:
+        raise ValueError(f"layer {layer} out of range for {layers} layers")
+    batch = write_blocks.shape[0]
+    for name, rows in (("write_blocks", write_blocks), ("write_slots", write_slots)):
+        if rows.dtype != torch.int32 or rows.dim() != 1 or rows.shape[0] != batch:
+            raise ValueError(f"{name} must be 1-D int32 with one entry per row")
+    if batch and write_blocks.stride(0) != write_slots.stride(0):
+        raise ValueError("write_blocks and write_slots must share one row stride")
+    expected = (batch, kv_heads, head_dim)
+    for name, t in (("k", k), ("v", v)):
+        if t.dtype != torch.bfloat16 or tuple(t.shape) != expected or not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous BF16 shaped {expected}")
+    devices = {device, write_blocks.device, write_slots.device, k.device, v.device}
+    if len(devices) != 1 or device.type != "cuda":
+        raise ValueError("the pool, rows, k and v must be on one GPU")
+    return batch
+
+
+def write_tokens(pool: torch.Tensor, write_blocks: torch.Tensor, write_slots: torch.Tensor, layer: int, k: torch.Tensor,
+                 v: torch.Tensor) -> None:
+    """The decode-time write of one token per row into a BF16 pool [blocks, 2, layers,
+    kv_heads, slots, head_dim], as one kernel: the same result as the reference's
+    pool[write_blocks, 0, layer, :, write_slots] = k and likewise for v (model.py:139-140).
+    Rows as for Fp8KVPool.write (int32, one shared stride, e.g. columns of decode_rows); ids
+    and slots are not checked against the pool. Enqueued on the current stream."""
+    if pool.dtype != torch.bfloat16 or pool.dim() != 6 or pool.shape[1] != KV_KINDS or not pool.is_contiguous():
+        raise ValueError("the pool must be a contiguous BF16 [blocks, 2, layers, kv_heads, slots, head_dim] tensor")
+    _, _, layers, kv_heads, slots, head_dim = pool.shape
+    batch = _check_token_write(pool.device, layers, kv_heads, head_dim, write_blocks, write_slots, layer, k, v)
+    if batch == 0:
+        return
+    _lib.check(
+        _lib.load().lk_kv_write(pool.data_ptr(), write_blocks.data_ptr(), write_slots.data_ptr(), write_blocks.stride(0), batch,
+                                k.data_ptr(), v.data_ptr(), layer, layers, kv_heads, slots, head_dim, _lib.current_stream(pool.device))
+    )
 
 
 def _is_fp8(pool) -> bool:

@@ -5,8 +5,8 @@ attention work per layer is tens of microseconds, so issuing each layer's launch
 Python sets the pace; a graph records a step's launches once and replays them as one. The
 reference captures its whole model step; the model is outside this package, so the unit
 captured here is the data path's share of a step: for every layer, the new token's K/V write
-into the pool (model.py:139-140, or Fp8KVPool.write for an FP8-resident pool) and paged decode
-attention over the block table.
+into the pool (model.py:139-140: hip_decode.write_tokens, or Fp8KVPool.write for an
+FP8-resident pool) and paged decode attention over the block table.
 
 As in the reference, each captured batch size gets fixed input tensors: one packed int32
 block of rows (write block, write slot, length, block table of fixed width, as
@@ -107,8 +107,7 @@ class DecodeAttentionGraphs:
             if isinstance(self.pool, Fp8KVPool):
                 self.pool.write(blocks, slots, layer, self.k_new[layer, :size], self.v_new[layer, :size])
             else:
-                self.pool[blocks.long(), 0, layer, :, slots.long()] = self.k_new[layer, :size]
-                self.pool[blocks.long(), 1, layer, :, slots.long()] = self.v_new[layer, :size]
+                hip_decode.write_tokens(self.pool, blocks, slots, layer, self.k_new[layer, :size], self.v_new[layer, :size])
             hip_decode.run_kernel(self.q[layer, :size], self.pool, layer, table, lengths, self.groups, out[layer], workspace)
         return out
 

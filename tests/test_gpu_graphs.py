@@ -237,3 +237,23 @@ def test_decode_reads_packed_row_columns_by_stride(fp8):
     assert torch.equal(strided.view(torch.int16), contiguous.view(torch.int16))
     rows = packed.cpu().numpy()
     assert_close(strided, oracle.decode_attention(q.float().cpu().numpy(), state, 20, rows[:, 3:], rows[:, 2], 4))
+
+
+def test_bf16_token_write_equals_the_reference_assignment():
+    """lk_kv_write against model.py:139-140's indexed assignment, from decode_rows columns."""
+    from layover_amd.config import ModelConfig
+    from layover_amd.kernels.hip_decode import write_tokens
+    from layover_amd.kv.paged_cache import BlockTable, PagedKVCache
+
+    cache = PagedKVCache(ModelConfig.qwen3_4b(), 12, device="cuda", fill=False)
+    cache.pool.copy_(torch.randn(cache.pool.shape, device="cuda").to(torch.bfloat16))
+    tables = [BlockTable([3, 7], 20), BlockTable([5], 1), BlockTable([1, 2, 9], 48), BlockTable([11], 16)]
+    packed = cache.decode_rows(tables).cuda()
+    k = torch.randn(4, 8, 128, device="cuda").to(torch.bfloat16)
+    v = torch.randn(4, 8, 128, device="cuda").to(torch.bfloat16)
+    expected = cache.pool.clone()
+    expected[packed[:, 0].long(), 0, 17, :, packed[:, 1].long()] = k
+    expected[packed[:, 0].long(), 1, 17, :, packed[:, 1].long()] = v
+    write_tokens(cache.pool, packed[:, 0], packed[:, 1], 17, k, v)
+    torch.cuda.synchronize()
+    assert torch.equal(cache.pool.view(torch.int16), expected.view(torch.int16))
