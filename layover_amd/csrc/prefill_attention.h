@@ -278,7 +278,8 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_mfma(PrefillArgs
 // distinct banks. Registers are held to 256 per lane (amdgpu_waves_per_eu(2)), so two
 // workgroups share a CU and one computes while the other waits at its step barrier: measured
 // on MI355X at a 2,048-token chunk ending a 32,768-token context, 2.97 ms per layer at one
-// wave per SIMD (268 registers) and 1.61 ms at two.
+// wave per SIMD (268 registers) and 1.61 ms at two; 1.51 ms with conflict-free LDS stores and
+// one FMA per weight's exponent.
 constexpr uint32_t kLdsWaves = 4;
 constexpr uint32_t kLdsRows = 32;                   // rows per wave
 constexpr uint32_t kLdsRowBytes = kDim * 2 + 16;    // 272
@@ -339,43 +340,50 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
         }
     }
 
-    // Cooperative step loads: thread t brings piece t % 64 of tile t / 64 (K0, K1, V0, V1):
-    // 64 bytes of BF16, or 32 FP8 codes that become 64 bytes of BF16 in LDS.
+    // Cooperative step loads: wave w brings tile w (K0, K1, V0, V1). Chunk x of lane t is
+    // values 512x + 8t .. +8 of the tile (16 bytes of BF16, or 8 FP8 codes that become 16
+    // bytes of BF16), so each wave-wide load reads 1 KiB (or 512 bytes) contiguous, and each
+    // LDS store fills whole 256-byte rows, 16 lanes a row: every bank once per 8 lanes.
     constexpr uint32_t kElem = KV == LK_FP8_RECORD ? 1 : 2;
     const uint32_t part = threadIdx.x / kWave;          // which tile
-    const uint32_t piece = threadIdx.x % kWave;         // which 32 values of it
+    const uint32_t piece = threadIdx.x % kWave;         // which 8 values of each 512
     const uint64_t tile_bytes = uint64_t(kSlots) * kDim * kElem;
     const uint64_t head_tile = uint64_t(a.layer) * a.kv_heads + kv_head;
     const uint64_t group = part < 2 ? head_tile : uint64_t(a.layers) * a.kv_heads + head_tile;
-    const uint64_t part_offset = group * tile_bytes + uint64_t(piece) * 32 * kElem;
+    const uint64_t part_offset = group * tile_bytes + uint64_t(piece) * 8 * kElem;
     const uint64_t block_elems = uint64_t(2) * a.layers * a.kv_heads * kSlots * kDim;
-    const uint32_t lds_offset = part * kLdsTile + (piece / 4) * kLdsRowBytes + (piece % 4) * 64;
+    // Value 512x + 8t sits in slot 4x + t / 16, dims 8 (t % 16) .. +8.
+    const uint32_t lds_offset = part * kLdsTile + (piece / 16) * kLdsRowBytes + (piece % 16) * 16;
     auto load_step = [&](uint32_t step, PrefillStaged& r) {
         const uint32_t block_index = min(2 * step + (part & 1), last_block);
         const int32_t block = a.block_ids[block_index];
-        const uint8_t* base = a.pool + uint64_t(uint32_t(block)) * a.block_bytes;
-        const u32x4* src = reinterpret_cast<const u32x4*>(base + part_offset);
+        const uint8_t* base = a.pool + uint64_t(uint32_t(block)) * a.block_bytes + part_offset;
         if constexpr (KV == LK_BF16) {
 #pragma unroll
-            for (int x = 0; x < 4; ++x) r.w[x] = src[x];
+            for (int x = 0; x < 4; ++x) r.w[x] = *reinterpret_cast<const u32x4*>(base + 1024 * x);
         } else {
-            r.w[0] = src[0];
-            r.w[1] = src[1];
-            r.shift = reinterpret_cast<const int16_t*>(base + block_elems)[group];
+#pragma unroll
+            for (int x = 0; x < 4; ++x) {
+                const u32x2 codes = *reinterpret_cast<const u32x2*>(base + 512 * x);
+                r.w[x / 2][2 * (x % 2)] = codes[0];
+                r.w[x / 2][2 * (x % 2) + 1] = codes[1];
+            }
+            r.shift = reinterpret_cast<const int16_t*>(a.pool + uint64_t(uint32_t(block)) * a.block_bytes + block_elems)[group];
         }
     };
     auto store_step = [&](uint32_t buffer, const PrefillStaged& r) {
-        u32x4* dst = reinterpret_cast<u32x4*>(lds[buffer] + lds_offset);
+        uint8_t* dst = lds[buffer] + lds_offset;
         if constexpr (KV == LK_BF16) {
 #pragma unroll
-            for (int x = 0; x < 4; ++x) dst[x] = r.w[x];
+            for (int x = 0; x < 4; ++x) *reinterpret_cast<u32x4*>(dst + 4 * kLdsRowBytes * x) = r.w[x];
         } else {
             const bool exact = !shift_is_exact_in_fp32(r.shift);
 #pragma unroll
             for (int x = 0; x < 4; ++x) {
                 const uint32_t lo = r.w[x / 2][2 * (x % 2)], hi = r.w[x / 2][2 * (x % 2) + 1];
-                dst[x] = u32x4{fp8_pair(lo, false, exact, r.shift), fp8_pair(lo, true, exact, r.shift), fp8_pair(hi, false, exact, r.shift),
-                               fp8_pair(hi, true, exact, r.shift)};
+                *reinterpret_cast<u32x4*>(dst + 4 * kLdsRowBytes * x) =
+                    u32x4{fp8_pair(lo, false, exact, r.shift), fp8_pair(lo, true, exact, r.shift), fp8_pair(hi, false, exact, r.shift),
+                          fp8_pair(hi, true, exact, r.shift)};
             }
             if (piece == 0) lds_shift[buffer][part] = r.shift;
         }
@@ -443,19 +451,24 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
                     if (key0 + b * kSlots + 4 * g + r >= end) rows[b][r] = u32x4{0u, 0u, 0u, 0u};
         }
 
+        // Softmax and PV for one row set. Row maxima are taken on the raw scores of each block
+        // and then scaled (the factors are positive), each weight's exponent is one FMA, and
+        // keys past the row's limit drop out. (A separate unmasked path for steps below every
+        // limit made the register allocator spill.) The V operand for output dim 8n + e is
+        // keys 4g..4g+3 of block 0 then of block 1, as four BF16 pairs.
+        auto attend = [&](int set) {
+            float top_b[2];
 #pragma unroll
-        for (int set = 0; set < 2; ++set) {
-            float score[8];
-#pragma unroll
-            for (int b = 0; b < 2; ++b)
+            for (int b = 0; b < 2; ++b) {
+                float t = -INFINITY;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int64_t key = int64_t(key0 + b * kSlots + 4 * g + r);
-                    score[4 * b + r] = key <= limit[set] ? s[set][b][r] * k_factor[b] : -INFINITY;
+                    const bool seen = int64_t(key0 + b * kSlots + 4 * g + r) <= limit[set];
+                    t = fmaxf(t, seen ? s[set][b][r] : -INFINITY);
                 }
-            float top = score[0];
-#pragma unroll
-            for (int i = 1; i < 8; ++i) top = fmaxf(top, score[i]);
+                top_b[b] = t * k_factor[b];
+            }
+            float top = fmaxf(top_b[0], top_b[1]);
             top = fmaxf(top, __shfl_xor(top, 16, kWave));
             top = fmaxf(top, __shfl_xor(top, 32, kWave));
             if (__builtin_expect(__any(top > m[set] + kRescaleThreshold), 0)) {
@@ -473,11 +486,14 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
             }
             float p[8];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                p[i] = score[i] == -INFINITY ? 0.0f : exp2_fast(score[i] - m[set]);
-                l[set] += p[i];
-                p[i] *= v_factor[i / 4];
-            }
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float w = exp2_fast(fmaf(s[set][b][r], k_factor[b], -m[set]));
+                    w = int64_t(key0 + b * kSlots + 4 * g + r) <= limit[set] ? w : 0.0f;
+                    l[set] += w;
+                    p[4 * b + r] = w * v_factor[b];
+                }
             const bf16x8 pb = as_bf16x8(pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]), pack_bf16(p[4], p[5]), pack_bf16(p[6], p[7]));
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
@@ -489,7 +505,11 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
                                             __builtin_amdgcn_perm(rows[1][3][w], rows[1][2][w], select));
                 o[set][e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pb, vb, o[set][e], 0, 0, 0);
             }
-        }
+        };
+        // A step wholly at or below the first live row's limit, and inside the chunk, needs no
+        // mask for any row of this wave (later rows only see more keys).
+        attend(0);
+        attend(1);
 
         // The next step's tiles into the other buffer; then the one after into registers.
         if (step + 1 < steps) {
