@@ -74,6 +74,19 @@ __device__ __forceinline__ float sum8(float v) {
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Max of a value over lanes n, n + 16, n + 32 and n + 48 (the four lane groups of an MFMA
+// result column), with gfx950's row-swapping permlanes instead of LDS-routed shuffles: given
+// the same register twice, permlane16_swap returns rows (0, 0, 2, 2) and (1, 1, 3, 3) of it,
+// and permlane32_swap rows (0, 1, 0, 1) and (2, 3, 2, 3).
+__device__ __forceinline__ float max_over_lane_groups(float value) {
+    const uint32_t bits = __float_as_uint(value);
+    const auto rows16 = __builtin_amdgcn_permlane16_swap(bits, bits, false, false);
+    const float half = fmaxf(__uint_as_float(rows16[0]), __uint_as_float(rows16[1]));
+    const uint32_t half_bits = __float_as_uint(half);
+    const auto rows32 = __builtin_amdgcn_permlane32_swap(half_bits, half_bits, false, false);
+    return fmaxf(__uint_as_float(rows32[0]), __uint_as_float(rows32[1]));
+}
+
 // Weight of a partial state with running max m against the merged max top; an empty state
 // (m = -inf) weighs nothing, even when every state is empty.
 __device__ __forceinline__ float merge_weight(float m, float top) { return m == -INFINITY ? 0.0f : exp2_fast(m - top); }

@@ -531,6 +531,7 @@ LK_EXPORT int lk_paged_prefill(const lk_prefill_shape* shape, const void* q, con
         lk::require(s.kv_format == LK_BF16 || s.kv_format == LK_FP8_RECORD, "paged prefill reads BF16 or FP8-record pools");
         const uint64_t end = uint64_t(s.start) + s.tokens;
         lk::require(uint64_t(num_block_ids) * s.slots >= end, "fewer block ids than the chunk's end needs");
+        lk::require(end <= 0x7FFFFFFFull, "a chunk must end below 2^31 tokens");
         lk_decode_shape d{};
         d.layers = s.layers;
         d.kv_heads = s.kv_heads;

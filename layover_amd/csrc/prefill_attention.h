@@ -279,7 +279,8 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_mfma(PrefillArgs
 // workgroups share a CU and one computes while the other waits at its step barrier: measured
 // on MI355X at a 2,048-token chunk ending a 32,768-token context, 2.97 ms per layer at one
 // wave per SIMD (268 registers) and 1.61 ms at two; 1.51 ms with conflict-free LDS stores and
-// one FMA per weight's exponent.
+// one FMA per weight's exponent; 1.39 ms with 32-bit causal compares, one mask per score and
+// the row maxima exchanged by permlane swaps instead of LDS-routed shuffles.
 constexpr uint32_t kLdsWaves = 4;
 constexpr uint32_t kLdsRows = 32;                   // rows per wave
 constexpr uint32_t kLdsRowBytes = kDim * 2 + 16;    // 272
@@ -318,7 +319,7 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
     const uint32_t last_block = (end + kSlots - 1) / kSlots - 1;
 
     // Per set: row n's token, head and causal limit; Q as the QK B operand.
-    int64_t limit[2];
+    int32_t limit[2];
     uint32_t qt[2][16];
 #pragma unroll
     for (int set = 0; set < 2; ++set) {
@@ -326,7 +327,7 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
         const bool live = row < total_rows;
         const uint32_t token = live ? row / a.groups : 0;
         const uint32_t head = kv_head * a.groups + (live ? row % a.groups : 0);
-        limit[set] = live ? int64_t(a.start) + token : -1;
+        limit[set] = live ? int32_t(a.start + token) : -1;
 #pragma unroll
         for (int i = 0; i < 16; ++i) qt[set][i] = 0;
         if (live) {
@@ -452,25 +453,26 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
         }
 
         // Softmax and PV for one row set. Row maxima are taken on the raw scores of each block
-        // and then scaled (the factors are positive), each weight's exponent is one FMA, and
-        // keys past the row's limit drop out. (A separate unmasked path for steps below every
-        // limit made the register allocator spill.) The V operand for output dim 8n + e is
-        // keys 4g..4g+3 of block 0 then of block 1, as four BF16 pairs.
+        // and then scaled (the factors are positive), and each weight's exponent is one FMA.
+        // (A separate unmasked path for steps below every limit made the register allocator
+        // spill.) The V operand for output dim 8n + e is keys 4g..4g+3 of block 0 then of
+        // block 1, as four BF16 pairs.
         auto attend = [&](int set) {
+            // Keys past the row's limit become -inf once, for the maximum and the weight alike
+            // (exp2(-inf) = 0: every live row sees key 0 in the first step, so m is finite).
+            float raw[2][4];
             float top_b[2];
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
                 float t = -INFINITY;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const bool seen = int64_t(key0 + b * kSlots + 4 * g + r) <= limit[set];
-                    t = fmaxf(t, seen ? s[set][b][r] : -INFINITY);
+                    raw[b][r] = int32_t(key0 + b * kSlots + 4 * g + r) <= limit[set] ? s[set][b][r] : -INFINITY;
+                    t = fmaxf(t, raw[b][r]);
                 }
                 top_b[b] = t * k_factor[b];
             }
-            float top = fmaxf(top_b[0], top_b[1]);
-            top = fmaxf(top, __shfl_xor(top, 16, kWave));
-            top = fmaxf(top, __shfl_xor(top, 32, kWave));
+            const float top = max_over_lane_groups(fmaxf(top_b[0], top_b[1]));
             if (__builtin_expect(__any(top > m[set] + kRescaleThreshold), 0)) {
                 asm volatile("" ::: "memory");
                 const float next = top > m[set] + kRescaleThreshold ? top : m[set];
@@ -489,8 +491,7 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
             for (int b = 0; b < 2; ++b)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    float w = exp2_fast(fmaf(s[set][b][r], k_factor[b], -m[set]));
-                    w = int64_t(key0 + b * kSlots + 4 * g + r) <= limit[set] ? w : 0.0f;
+                    const float w = exp2_fast(fmaf(raw[b][r], k_factor[b], -m[set]));
                     l[set] += w;
                     p[4 * b + r] = w * v_factor[b];
                 }
