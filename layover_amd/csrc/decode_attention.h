@@ -399,9 +399,7 @@ __global__ __launch_bounds__(kWave* kDecodeWaves) void decode_split_mfma(DecodeA
         float score[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) score[r] = token0 + 4 * g + r < uint32_t(length) ? s[r] * k_factor : -INFINITY;
-        float top = fmaxf(fmaxf(score[0], score[1]), fmaxf(score[2], score[3]));
-        top = fmaxf(top, __shfl_xor(top, 16, kWave));
-        top = fmaxf(top, __shfl_xor(top, 32, kWave));
+        const float top = max_over_lane_groups(fmaxf(fmaxf(score[0], score[1]), fmaxf(score[2], score[3])));
         // Raise the running max only when a score passes it by more than 2^8.
         if (__builtin_expect(__any(top > m + kRescaleThreshold), 0)) {
             // Kept as a branch: flattened, its multiplies would run on every unit.

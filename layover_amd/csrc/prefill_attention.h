@@ -182,9 +182,7 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_mfma(PrefillArgs
         float score[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) score[r] = int64_t(key0 + 4 * g + r) <= limit ? s[r] * k_factor : -INFINITY;
-        float top = fmaxf(fmaxf(score[0], score[1]), fmaxf(score[2], score[3]));
-        top = fmaxf(top, __shfl_xor(top, 16, kWave));
-        top = fmaxf(top, __shfl_xor(top, 32, kWave));
+        const float top = max_over_lane_groups(fmaxf(fmaxf(score[0], score[1]), fmaxf(score[2], score[3])));
         if (__builtin_expect(__any(top > m + kRescaleThreshold), 0)) {
             asm volatile("" ::: "memory");
             const float next = top > m + kRescaleThreshold ? top : m;
