@@ -115,3 +115,35 @@ def test_decode_launch_layout_takes_packed_columns_and_refuses_what_it_cannot_de
         hip_decode._check_layout(q, table, lengths[:2], q.clone())
     with pytest.raises(ValueError, match="contiguous tensors"):
         hip_decode._check_layout(q, table, lengths, q.transpose(0, 1).contiguous().transpose(0, 1))
+
+
+def test_token_write_and_prefill_arguments_are_checked_without_a_gpu():
+    """The metadata checks run before any launch, so they refuse CPU tensors and bad shapes
+    on any machine."""
+    from layover_amd.kernels import hip_decode, hip_prefill
+
+    rows = torch.zeros(2, dtype=torch.int32)
+    k = torch.zeros(2, 8, 128, dtype=torch.bfloat16)
+    pool = torch.zeros(4, 2, 3, 8, 16, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="one GPU"):
+        hip_decode.write_tokens(pool, rows, rows, 0, k, k)
+    with pytest.raises(ValueError, match="layer"):
+        hip_decode.write_tokens(pool, rows, rows, 3, k, k)
+    with pytest.raises(ValueError, match="int32"):
+        hip_decode.write_tokens(pool, rows.long(), rows, 0, k, k)
+    with pytest.raises(ValueError, match="row stride"):
+        packed = torch.zeros(2, 5, dtype=torch.int32)
+        hip_decode.write_tokens(pool, packed[:, 0], torch.zeros(2, dtype=torch.int32), 0, k, k)
+    with pytest.raises(ValueError, match="BF16"):
+        hip_decode.write_tokens(pool, rows, rows, 0, k.float(), k)
+    with pytest.raises(ValueError, match="contiguous BF16"):
+        hip_decode.write_tokens(pool.float(), rows, rows, 0, k, k)
+
+    q = torch.zeros(32, 10, 128, dtype=torch.bfloat16)
+    ids = torch.arange(4, dtype=torch.int32)
+    with pytest.raises(ValueError, match="one GPU"):
+        hip_prefill.paged_prefill_attention_hip(q, pool, 0, ids, 0, 4)
+    with pytest.raises(ValueError, match="16-slot blocks of 128"):
+        hip_prefill.paged_prefill_attention_hip(q[..., :64].contiguous(), pool[..., :64].contiguous(), 0, ids, 0, 4)
+    with pytest.raises(ValueError, match="cannot hold"):
+        hip_prefill.paged_prefill_attention_hip(q, pool, 0, ids[:1], 10, 4)
