@@ -446,7 +446,9 @@ __global__ __launch_bounds__(kWave* kDecodeWaves) void decode_split_mfma(DecodeA
             const uint32_t b23 = __builtin_amdgcn_perm(v[3][e / 2], v[2][e / 2], select);
             const s16x4 vb = __builtin_bit_cast(s16x4, u32x2{b01, b23});
             o[e] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(p_hi, vb, o[e], 0, 0, 0);
-            o[e] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(p_lo, vb, o[e], 0, 0, 0);
+            // The low half carries the weights' bits below BF16; FP8 values (3 significand
+            // bits) do without it, and the FP8 kernel is not HBM-bound without it.
+            if constexpr (KV == LK_BF16) o[e] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(p_lo, vb, o[e], 0, 0, 0);
         }
     };
 
