@@ -117,6 +117,12 @@ int lt_host_set_paused(lt_engine* engine, int paused);
 int lt_host_set_copy_delay_us(lt_engine* engine, uint32_t delay_us);
 int lt_host_set_pin_limit(lt_engine* engine, uint64_t bytes);
 
+/* No counterpart in the reference. Copies to the host that the HIP flavour has run on an SDMA
+ * engine (hsa_amd_memory_async_copy) since the library was loaded; the host flavour returns 0.
+ * With LAYOVER_D2H=sdma in the environment, copies of at least 4 MiB from HIP device memory
+ * into pinned host memory take that path; otherwise every copy uses hipMemcpyAsync. */
+uint64_t lt_sdma_copies(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -29,3 +29,5 @@ LT_EXPORT int lt_host_set_copy_delay_us(lt_engine* engine, uint32_t delay_us) {
 LT_EXPORT int lt_host_set_pin_limit(lt_engine* engine, uint64_t bytes) {
     return lt::guarded(engine, [&] { engine->impl.device().set_pin_limit(bytes); });
 }
+
+LT_EXPORT uint64_t lt_sdma_copies(void) { return 0; }

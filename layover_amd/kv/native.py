@@ -98,13 +98,14 @@ def build_host() -> Path:
     return library_path("host")
 
 
-def hip_runtimes_loaded() -> list[str]:
-    """Paths of every libamdhip64 mapped into this process; exactly one is safe."""
+def hip_runtimes_loaded(name: str = "libamdhip64") -> list[str]:
+    """Paths of every libamdhip64 (or other runtime `name`) mapped into this process; exactly
+    one is safe."""
     seen = []
     with open("/proc/self/maps") as maps:
         for line in maps:
             path = line.split()[-1] if "/" in line else ""
-            if "libamdhip64" in path and path not in seen:
+            if name in path and path not in seen:
                 seen.append(path)
     return seen
 
@@ -130,9 +131,16 @@ def load_library(flavor: str, path: Path | str | None = None) -> ctypes.CDLL:
         raise NativeUnavailable(f"{path} cannot be loaded: {error}") from error
     if flavor == "hip" and len(hip_runtimes_loaded()) > 1:
         raise NativeUnavailable(f"two HIP runtimes are loaded: {hip_runtimes_loaded()}")
+    if flavor == "hip" and len(hip_runtimes_loaded("libhsa-runtime64")) > 1:
+        # A profiler maps a second HSA runtime beside the one HIP runs on; SDMA copies issued
+        # through it would not know HIP's allocations, so copies to the host stay with HIP.
+        os.environ.pop("LAYOVER_D2H", None)
     lib.lt_abi_version.restype = c_int
     lib.lt_flavor.restype = c_char_p
     lib.lt_last_error.restype = c_char_p
+    if hasattr(lib, "lt_sdma_copies"):  # this build's extension; the reference's library lacks it
+        lib.lt_sdma_copies.restype = ctypes.c_uint64
+        lib.lt_sdma_copies.argtypes = []
     if lib.lt_abi_version() != ABI_VERSION:
         raise NativeUnavailable(f"{path} has ABI {lib.lt_abi_version()}, expected {ABI_VERSION}: rebuild it")
     built = lib.lt_flavor().decode()
