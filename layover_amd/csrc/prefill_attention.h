@@ -260,30 +260,49 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_mfma(PrefillArgs
 }
 
 // ---------------------------------------------------------------------------------------
-// BF16 pools: K/V shared through LDS. A workgroup of 4 waves owns 128 rows (32 per wave, as
-// two sets of 16) and walks the keys in steps of 32 (two blocks). Each step's K and V tiles
-// (4 x 4 KiB) are loaded once per workgroup, every thread bringing 64 contiguous bytes, into
-// one of two LDS buffers while the other is read; the next step's bytes are already in
-// registers, loaded one step ahead. Per wave and step:
+// K/V shared through LDS. A workgroup of 4 waves owns 128 rows (32 per wave, as two sets of
+// 16) and walks the keys in steps of 32 (two blocks). Each step's K and V tiles (4 x 4 KiB)
+// are loaded once per workgroup, every thread bringing 64 contiguous bytes, into one of two
+// LDS buffers while the other is read; the next step's bytes are already in registers, loaded
+// one step ahead. Per wave and step:
 //   QK   for each block and set, four v_mfma_f32_16x16x32_bf16 on K read from LDS (lane
 //        (g, n): key n, dims 32g + 8j .. +8), reused by both sets;
 //   P    8 scores per lane (keys 4g..4g+3 of each block) of row n;
-//   PV   v_mfma_f32_16x16x32_bf16 over the step's 32 keys: the MFMA's k index 8g + i stands
-//        for key 4g + i of block 0 (i < 4) or of block 1 (i >= 4), in both P (the lane's
-//        own 8 weights, as BF16) and V (read from LDS as 16-byte rows of 8 dims, regrouped by
-//        v_perm per output dim), reused by both sets.
-// LDS rows are padded to 272 bytes so the 16 lanes reading one column of 16 rows hit
-// distinct banks. Registers are held to 256 per lane (amdgpu_waves_per_eu(2)), so two
-// workgroups share a CU and one computes while the other waits at its step barrier: measured
-// on MI355X at a 2,048-token chunk ending a 32,768-token context, 2.97 ms per layer at one
-// wave per SIMD (268 registers) and 1.61 ms at two; 1.51 ms with conflict-free LDS stores and
-// one FMA per weight's exponent; 1.39 ms with 32-bit causal compares, one mask per score and
-// the row maxima exchanged by permlane swaps instead of LDS-routed shuffles.
+//   PV   v_mfma_f32_16x16x32_bf16 over the step's 32 keys for output dims 16e .. 16e+15: the
+//        MFMA's k index 8g + i stands for key 4g + i of block 0 (i < 4) or of block 1
+//        (i >= 4), in both P (the lane's own 8 weights, as BF16) and V. V stays row-major in
+//        LDS (a key per row) and reaches the B operand through the transposing read
+//        ds_read_b64_tr_b16: within a 16-lane group, lane i receives element i % 4 of the
+//        8-byte rows fetched by lanes i / 4 + 4t (t = 0..3). Lane 4t + q of group g fetches
+//        key 4g + t, dims 16e + 4q .. +3, so lane n receives keys 4g..4g+3 of dim 16e + n,
+//        which is its B operand half for that block, with no register shuffles.
+//   sum  BF16 pools: the weight sums come from one more MFMA of P against a B of ones, so
+//        they land in the layout of O (lane (g, n): rows 4g + r) and use the same rounded
+//        weights as the numerator. FP8 pools weight P by the V block's 2^shift, so their
+//        sums stay per-lane VALU adds of the unscaled weights.
+// Causal masking runs only in steps that reach past the wave's first row's limit (the later
+// rows of a wave only see more keys). K rows are padded to 272 bytes, so the 16 lanes reading
+// one column of 16 rows with 16-byte reads hit distinct banks; V rows to 288 bytes, so the 16
+// lanes of a group fetching 8 bytes from 4 rows at 4 offsets cover 32 distinct banks.
+// Registers are held to 256 per lane (amdgpu_waves_per_eu(2)), so two workgroups share a CU
+// and one computes while the other waits at its step barrier. Measured on MI355X at a
+// 2,048-token chunk ending a 32,768-token context: 2.97 ms per layer at one wave per SIMD and
+// 1.61 ms at two; 1.39 ms with conflict-free LDS stores, one FMA per weight's exponent, 32-bit
+// causal compares and permlane-swapped row maxima, with V regrouped by 32 v_perm per step.
+// O leaves through LDS: its rows are spread over lanes by dim (16e + n), so each wave writes
+// its 32 rows there and reads them back as 16-byte pieces of whole rows.
 constexpr uint32_t kLdsWaves = 4;
-constexpr uint32_t kLdsRows = 32;                   // rows per wave
-constexpr uint32_t kLdsRowBytes = kDim * 2 + 16;    // 272
-constexpr uint32_t kLdsTile = kSlots * kLdsRowBytes; // one block's K or V
-constexpr uint32_t kLdsStep = 4 * kLdsTile;          // K0, K1, V0, V1
+constexpr uint32_t kLdsRows = 32;                       // rows per wave
+constexpr uint32_t kLdsRowBytes = kDim * 2 + 16;        // 272: K rows
+constexpr uint32_t kLdsVRowBytes = kDim * 2 + 32;       // 288: V rows
+constexpr uint32_t kLdsTile = kSlots * kLdsRowBytes;    // one block's K
+constexpr uint32_t kLdsVTile = kSlots * kLdsVRowBytes;  // one block's V
+constexpr uint32_t kLdsStep = 2 * kLdsTile + 2 * kLdsVTile;  // K0, K1, V0, V1
+constexpr uint32_t kLdsBuffers = 2;  // step i is read from one while step i + 1 is stored
+static_assert(kLdsWaves * kLdsRows * kLdsRowBytes <= kLdsBuffers * kLdsStep, "the output staging must fit the step buffers");
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 // FP8-record pools: each thread converts its 32 codes to BF16 as it stages them (the exact
 // hardware convert), and each block's 2^shift is applied to that block's scores (K) and
@@ -297,8 +316,8 @@ struct PrefillStaged {
 
 template <int KV>
 __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_mfma_lds(PrefillArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2][kLdsStep];
-    __shared__ int32_t lds_shift[2][4];  // FP8: per buffer, the shift of K0, K1, V0, V1
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBuffers][kLdsStep];
+    __shared__ int32_t lds_shift[kLdsBuffers][4];  // FP8: per buffer, the shift of K0, K1, V0, V1
     const uint32_t lane = threadIdx.x % kWave;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const uint32_t g = lane / 16;
@@ -315,6 +334,8 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
     const uint32_t key_blocks = (a.start + wg_last / a.groups) / kSlots + 1;
     const uint32_t steps = (key_blocks + 1) / 2;
     const uint32_t last_block = (end + kSlots - 1) / kSlots - 1;
+    // The wave's first row's limit (later rows only see more keys); -1 for a wave past the end.
+    const int64_t first_limit = row0 < total_rows ? int64_t(a.start) + row0 / a.groups : -1;
 
     // Per set: row n's token, head and causal limit; Q as the QK B operand.
     int32_t limit[2];
@@ -342,7 +363,7 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
     // Cooperative step loads: wave w brings tile w (K0, K1, V0, V1). Chunk x of lane t is
     // values 512x + 8t .. +8 of the tile (16 bytes of BF16, or 8 FP8 codes that become 16
     // bytes of BF16), so each wave-wide load reads 1 KiB (or 512 bytes) contiguous, and each
-    // LDS store fills whole 256-byte rows, 16 lanes a row: every bank once per 8 lanes.
+    // LDS store fills whole 256-byte rows, 16 lanes a row.
     constexpr uint32_t kElem = KV == LK_FP8_RECORD ? 1 : 2;
     const uint32_t part = threadIdx.x / kWave;          // which tile
     const uint32_t piece = threadIdx.x % kWave;         // which 8 values of each 512
@@ -352,7 +373,9 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
     const uint64_t part_offset = group * tile_bytes + uint64_t(piece) * 8 * kElem;
     const uint64_t block_elems = uint64_t(2) * a.layers * a.kv_heads * kSlots * kDim;
     // Value 512x + 8t sits in slot 4x + t / 16, dims 8 (t % 16) .. +8.
-    const uint32_t lds_offset = part * kLdsTile + (piece / 16) * kLdsRowBytes + (piece % 16) * 16;
+    const uint32_t row_bytes = part < 2 ? kLdsRowBytes : kLdsVRowBytes;
+    const uint32_t lds_offset =
+        (part < 2 ? part * kLdsTile : 2 * kLdsTile + (part - 2) * kLdsVTile) + (piece / 16) * row_bytes + (piece % 16) * 16;
     auto load_step = [&](uint32_t step, PrefillStaged& r) {
         const uint32_t block_index = min(2 * step + (part & 1), last_block);
         const int32_t block = a.block_ids[block_index];
@@ -374,13 +397,13 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
         uint8_t* dst = lds[buffer] + lds_offset;
         if constexpr (KV == LK_BF16) {
 #pragma unroll
-            for (int x = 0; x < 4; ++x) *reinterpret_cast<u32x4*>(dst + 4 * kLdsRowBytes * x) = r.w[x];
+            for (int x = 0; x < 4; ++x) *reinterpret_cast<u32x4*>(dst + 4 * row_bytes * x) = r.w[x];
         } else {
             const bool exact = !shift_is_exact_in_fp32(r.shift);
 #pragma unroll
             for (int x = 0; x < 4; ++x) {
                 const uint32_t lo = r.w[x / 2][2 * (x % 2)], hi = r.w[x / 2][2 * (x % 2) + 1];
-                *reinterpret_cast<u32x4*>(dst + 4 * kLdsRowBytes * x) =
+                *reinterpret_cast<u32x4*>(dst + 4 * row_bytes * x) =
                     u32x4{fp8_pair(lo, false, exact, r.shift), fp8_pair(lo, true, exact, r.shift), fp8_pair(hi, false, exact, r.shift),
                           fp8_pair(hi, true, exact, r.shift)};
             }
@@ -388,155 +411,245 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
         }
     };
 
+    // Running maximum per row (lane (g, n): row n of each set); output and, for BF16 pools,
+    // weight sums in the MFMA output layout (lane (g, n): rows 4g + r, dims 16e + n).
     float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
-    f32x4 o[2][8];
+    f32x4 o[2][8], sums[2];
 #pragma unroll
-    for (int set = 0; set < 2; ++set)
+    for (int set = 0; set < 2; ++set) {
+        sums[set] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[set][e] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    const bf16x8 ones = as_bf16x8(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
 
-    PrefillStaged staged;
-    load_step(0, staged);
-    store_step(0, staged);
-    if (steps > 1) load_step(1, staged);
-    __syncthreads();
+    // Transposing V reads: lane 4t + q of group g fetches key 4g + t, dims 16e + 4q .. +3.
+    const uint32_t v_read = 2 * kLdsTile + (4 * g + n / 4) * kLdsVRowBytes + (n % 4) * 8;
 
-    for (uint32_t step = 0; step < steps; ++step) {
-        const uint8_t* buf = lds[step & 1];
-        const uint32_t key0 = step * 2 * kSlots;
-        float k_factor[2] = {a.scale_log2, a.scale_log2}, v_factor[2] = {1.0f, 1.0f};
+    // Per step: the scale of each block's scores (log2 units) and of its weights.
+    struct Factors {
+        float k[2];
+        float v[2];
+    };
+    auto factors = [&](uint32_t step) {
+        Factors f{{a.scale_log2, a.scale_log2}, {1.0f, 1.0f}};
         if constexpr (KV == LK_FP8_RECORD) {
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
-                const int32_t ks = lds_shift[step & 1][b], vs = lds_shift[step & 1][2 + b];
-                if (shift_is_exact_in_fp32(ks)) k_factor[b] *= pow2(ks);
-                if (shift_is_exact_in_fp32(vs)) v_factor[b] = pow2(vs);
+                const int32_t ks = lds_shift[step % kLdsBuffers][b], vs = lds_shift[step % kLdsBuffers][2 + b];
+                if (shift_is_exact_in_fp32(ks)) f.k[b] *= pow2(ks);
+                if (shift_is_exact_in_fp32(vs)) f.v[b] = pow2(vs);
             }
         }
+        return f;
+    };
 
-        // Scores S^T = K Q^T for both blocks and both sets.
-        f32x4 s[2][2];
+    // K of a step as A operands (lane (g, n): key n, dims 32g + 8j .. +8), then one set's scores
+    // S^T = K Q^T for both blocks.
+    auto read_k = [&](uint32_t step, bf16x8 (&kk)[2][4]) {
+        const uint8_t* buf = lds[step % kLdsBuffers];
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             const uint8_t* k_row = buf + b * kLdsTile + n * kLdsRowBytes + 64 * g;
-            bf16x8 kk[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) kk[j] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(k_row + 16 * j));
-#pragma unroll
-            for (int set = 0; set < 2; ++set) {
-                f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        kk[j], as_bf16x8(qt[set][4 * j], qt[set][4 * j + 1], qt[set][4 * j + 2], qt[set][4 * j + 3]), acc, 0, 0, 0);
-                s[set][b] = acc;
-            }
+            for (int j = 0; j < 4; ++j) kk[b][j] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(k_row + 16 * j));
         }
+    };
+    auto scores = [&](int set, const bf16x8 (&kk)[2][4], f32x4 (&s)[2]) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    kk[b][j], as_bf16x8(qt[set][4 * j], qt[set][4 * j + 1], qt[set][4 * j + 2], qt[set][4 * j + 3]), acc, 0, 0, 0);
+            s[b] = acc;
+        }
+    };
 
-        // V of the step as B operands: for output dim 8n + e, the values of keys
-        // (4g + r of block 0, then of block 1), as four BF16 pairs.
-        u32x4 rows[2][4];
+    // V of a step as B operands, one per 16 output dims: keys 4g..4g+3 of block 0, then of
+    // block 1, for dim 16e + n, as four BF16 pairs.
+    auto values = [&](uint32_t step, u32x4 (&vb)[8]) {
+        const auto* buf = (const __attribute__((address_space(3))) uint8_t*)(lds[step % kLdsBuffers]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const auto* at = buf + v_read + 32 * e;
+            const i16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(at));
+            const i16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(at + kLdsVTile));
+            const u32x2 w0 = __builtin_bit_cast(u32x2, v0), w1 = __builtin_bit_cast(u32x2, v1);
+            vb[e] = u32x4{w0[0], w0[1], w1[0], w1[1]};
+        }
+    };
+
+    // Keys past a row's limit become -inf, for the maximum and the weight alike (exp2(-inf)
+    // = 0: every live row sees key 0 in the first step, so m is finite).
+    auto mask = [&](uint32_t step, int set, f32x4 (&s)[2]) {
+        const uint32_t key0 = step * 2 * kSlots;
 #pragma unroll
         for (int b = 0; b < 2; ++b)
 #pragma unroll
             for (int r = 0; r < 4; ++r)
-                rows[b][r] = *reinterpret_cast<const u32x4*>(buf + (2 + b) * kLdsTile + (4 * g + r) * kLdsRowBytes + 16 * n);
-        // Keys at or past the chunk's end hold anything: zero their V (0 * NaN is NaN).
-        if (key0 + 2 * kSlots > end) {
-#pragma unroll
-            for (int b = 0; b < 2; ++b)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    if (key0 + b * kSlots + 4 * g + r >= end) rows[b][r] = u32x4{0u, 0u, 0u, 0u};
-        }
+                if (int32_t(key0 + b * kSlots + 4 * g + r) > limit[set]) s[b][r] = -INFINITY;
+    };
 
-        // Softmax and PV for one row set. Row maxima are taken on the raw scores of each block
-        // and then scaled (the factors are positive), and each weight's exponent is one FMA.
-        // (A separate unmasked path for steps below every limit made the register allocator
-        // spill.) The V operand for output dim 8n + e is keys 4g..4g+3 of block 0 then of
-        // block 1, as four BF16 pairs.
-        auto attend = [&](int set) {
-            // Keys past the row's limit become -inf once, for the maximum and the weight alike
-            // (exp2(-inf) = 0: every live row sees key 0 in the first step, so m is finite).
-            float raw[2][4];
-            float top_b[2];
+    // Row maximum of one set's scores, taken on the raw scores of each block and then scaled
+    // (the factors are positive). The state is rescaled only when a maximum grows by more than
+    // kRescaleThreshold, which is rare after the first steps.
+    auto row_max = [&](const f32x4 (&s)[2], const Factors& f) {
+        float top_b[2];
 #pragma unroll
-            for (int b = 0; b < 2; ++b) {
-                float t = -INFINITY;
+        for (int b = 0; b < 2; ++b) top_b[b] = fmaxf(fmaxf(fmaxf(s[b][0], s[b][1]), s[b][2]), s[b][3]) * f.k[b];
+        return max_over_lane_groups(fmaxf(top_b[0], top_b[1]));
+    };
+    auto rescale = [&](const float (&top)[2]) {
+        if (__builtin_expect(__any(top[0] > m[0] + kRescaleThreshold || top[1] > m[1] + kRescaleThreshold), 0)) {
+            asm volatile("" ::: "memory");
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    raw[b][r] = int32_t(key0 + b * kSlots + 4 * g + r) <= limit[set] ? s[set][b][r] : -INFINITY;
-                    t = fmaxf(t, raw[b][r]);
-                }
-                top_b[b] = t * k_factor[b];
-            }
-            const float top = max_over_lane_groups(fmaxf(top_b[0], top_b[1]));
-            if (__builtin_expect(__any(top > m[set] + kRescaleThreshold), 0)) {
-                asm volatile("" ::: "memory");
-                const float next = top > m[set] + kRescaleThreshold ? top : m[set];
+            for (int set = 0; set < 2; ++set) {
+                const float next = top[set] > m[set] + kRescaleThreshold ? top[set] : m[set];
                 const float alpha = merge_weight(m[set], next);
                 m[set] = next;
                 l[set] *= alpha;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const float factor = __shfl(alpha, int(4 * g + r), kWave);
+                    sums[set][r] *= factor;
 #pragma unroll
                     for (int e = 0; e < 8; ++e) o[set][e][r] *= factor;
                 }
             }
-            float p[8];
-#pragma unroll
-            for (int b = 0; b < 2; ++b)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float w = exp2_fast(fmaf(raw[b][r], k_factor[b], -m[set]));
-                    l[set] += w;
-                    p[4 * b + r] = w * v_factor[b];
-                }
-            const bf16x8 pb = as_bf16x8(pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]), pack_bf16(p[4], p[5]), pack_bf16(p[6], p[7]));
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint32_t select = (e & 1) ? 0x07060302u : 0x05040100u;
-                const uint32_t w = e / 2;
-                const bf16x8 vb = as_bf16x8(__builtin_amdgcn_perm(rows[0][1][w], rows[0][0][w], select),
-                                            __builtin_amdgcn_perm(rows[0][3][w], rows[0][2][w], select),
-                                            __builtin_amdgcn_perm(rows[1][1][w], rows[1][0][w], select),
-                                            __builtin_amdgcn_perm(rows[1][3][w], rows[1][2][w], select));
-                o[set][e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pb, vb, o[set][e], 0, 0, 0);
-            }
-        };
-        // A step wholly at or below the first live row's limit, and inside the chunk, needs no
-        // mask for any row of this wave (later rows only see more keys).
-        attend(0);
-        attend(1);
+        }
+    };
 
-        // The next step's tiles into the other buffer; then the one after into registers.
+    // One set's weights as a BF16 A operand (each exponent one FMA); FP8 pools weight each
+    // block by its V factor and keep the unscaled sums per lane.
+    auto weights = [&](int set, const f32x4 (&s)[2], const Factors& f) {
+        float p[8];
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float w = exp2_fast(fmaf(s[b][r], f.k[b], -m[set]));
+                if constexpr (KV == LK_BF16) {
+                    p[4 * b + r] = w;
+                } else {
+                    l[set] += w;
+                    p[4 * b + r] = w * f.v[b];
+                }
+            }
+        return as_bf16x8(pack_bf16(p[0], p[1]), pack_bf16(p[2], p[3]), pack_bf16(p[4], p[5]), pack_bf16(p[6], p[7]));
+    };
+
+    // One set's PV (and, for BF16 pools, its weight sums).
+    auto accumulate = [&](int set, const bf16x8& pb, const u32x4 (&vb)[8]) {
+        if constexpr (KV == LK_BF16) sums[set] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pb, ones, sums[set], 0, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            o[set][e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pb, __builtin_bit_cast(bf16x8, vb[e]), o[set][e], 0, 0, 0);
+    };
+
+    PrefillStaged staged;
+    // One step, per set: scores, mask and maximum, then (after a rare rescale of both sets)
+    // weights and PV, in two straight stretches that the scheduler fills from both sets. Then
+    // the next step's tiles go into the other buffer and the one after into registers. Steps
+    // that need the causal mask (and the chunk-end V mask, which only the last step can need)
+    // run in a second copy of the loop. Forcing an MFMA/VALU interleave with scheduling
+    // barriers measured 4% slower: the two waves on each SIMD already overlap each other.
+    auto run_step = [&](uint32_t step, auto masked_tag) {
+        constexpr bool kMasked = decltype(masked_tag)::value;
+        const Factors f = factors(step);
+        bf16x8 kk[2][4];
+        read_k(step, kk);
+        u32x4 vb[8];
+        values(step, vb);
+        f32x4 s[2][2];
+        scores(0, kk, s[0]);
+        scores(1, kk, s[1]);
+        if constexpr (kMasked) mask(step, 0, s[0]);
+        float top[2];
+        top[0] = row_max(s[0], f);
+        if constexpr (kMasked) {
+            mask(step, 1, s[1]);
+            // Keys at or past the chunk's end hold anything: zero their V (0 * NaN is NaN).
+            const uint32_t key0 = step * 2 * kSlots;
+            if (key0 + 2 * kSlots > end) {
+#pragma unroll
+                for (int b = 0; b < 2; ++b) {
+                    const int32_t first = int32_t(key0 + b * kSlots + 4 * g);
+                    const int32_t valid = min(max(int32_t(end) - first, 0), 4);
+                    const uint32_t lo = valid >= 2 ? 0xFFFFFFFFu : valid == 1 ? 0x0000FFFFu : 0u;
+                    const uint32_t hi = valid >= 4 ? 0xFFFFFFFFu : valid == 3 ? 0x0000FFFFu : 0u;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        vb[e][2 * b] &= lo;
+                        vb[e][2 * b + 1] &= hi;
+                    }
+                }
+            }
+        }
+        top[1] = row_max(s[1], f);
+        rescale(top);
+        const bf16x8 p0 = weights(0, s[0], f);
+        accumulate(0, p0, vb);
+        const bf16x8 p1 = weights(1, s[1], f);
+        accumulate(1, p1, vb);
         if (step + 1 < steps) {
-            store_step((step + 1) & 1, staged);
+            store_step((step + 1) % kLdsBuffers, staged);
             if (step + 2 < steps) load_step(step + 2, staged);
         }
         __syncthreads();
-    }
+    };
 
+    load_step(0, staged);
+    store_step(0, staged);
+    if (steps > 1) load_step(1, staged);
+    __syncthreads();
+    // Steps whose 32 keys all lie at or below the wave's first row's limit need no mask.
+    const uint32_t unmasked = first_limit < 0 ? 0u : min(steps, uint32_t((first_limit + 1) / (2 * kSlots)));
+    uint32_t step = 0;
+    for (; step < unmasked; ++step) run_step(step, std::false_type{});
+    for (; step < steps; ++step) run_step(step, std::true_type{});
+
+    // Row totals in the layout of O: lane (g, n) needs rows 4g + r. FP8 pools summed per lane
+    // (row n, a quarter of the keys each): reduce over the lane groups, then fetch row 4g + r.
+    float inverse[2][4];
 #pragma unroll
     for (int set = 0; set < 2; ++set) {
-        float total = l[set];
-        total += __shfl_xor(total, 16, kWave);
-        total += __shfl_xor(total, 32, kWave);
-        const float inverse = 1.0f / total;
+        if constexpr (KV == LK_BF16) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const float factor = __shfl(inverse, int(4 * g + r), kWave);
-            const uint32_t out_row = row0 + 16 * set + 4 * g + r;
-            if (out_row < total_rows) {
-                const uint32_t out_token = out_row / a.groups;
-                const uint32_t out_head = kv_head * a.groups + out_row % a.groups;
-                u32x4 packed;
+            for (int r = 0; r < 4; ++r) inverse[set][r] = 1.0f / sums[set][r];
+        } else {
+            float total = l[set];
+            total += __shfl_xor(total, 16, kWave);
+            total += __shfl_xor(total, 32, kWave);
+            const float own = 1.0f / total;
 #pragma unroll
-                for (int x = 0; x < 4; ++x)
-                    packed[x] = uint32_t(to_bf16(o[set][2 * x][r] * factor)) | (uint32_t(to_bf16(o[set][2 * x + 1][r] * factor)) << 16);
-                *reinterpret_cast<u32x4*>(a.out + (uint64_t(out_head) * a.tokens + out_token) * kDim + 8 * n) = packed;
-            }
+            for (int r = 0; r < 4; ++r) inverse[set][r] = __shfl(own, int(4 * g + r), kWave);
+        }
+    }
+
+    // O through LDS (the loop's last barrier has released the buffers): row 16 set + 4g + r,
+    // dim 16e + n of this wave's 32 rows, then whole rows out in 16-byte pieces.
+    uint8_t* staging = &lds[0][0] + wave * kLdsRows * kLdsRowBytes;
+#pragma unroll
+    for (int set = 0; set < 2; ++set)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                *reinterpret_cast<uint16_t*>(staging + (16 * set + 4 * g + r) * kLdsRowBytes + (16 * e + n) * 2) =
+                    to_bf16(o[set][e][r] * inverse[set][r]);
+    __syncthreads();
+#pragma unroll
+    for (int x = 0; x < 8; ++x) {
+        const uint32_t piece_index = lane + kWave * x;  // 16 pieces of 8 dims per row
+        const uint32_t local_row = piece_index / 16;
+        const uint32_t out_row = row0 + local_row;
+        if (out_row < total_rows) {
+            const uint32_t out_token = out_row / a.groups;
+            const uint32_t out_head = kv_head * a.groups + out_row % a.groups;
+            *reinterpret_cast<u32x4*>(a.out + (uint64_t(out_head) * a.tokens + out_token) * kDim + 8 * (piece_index % 16)) =
+                *reinterpret_cast<const u32x4*>(staging + local_row * kLdsRowBytes + 16 * (piece_index % 16));
         }
     }
 }
