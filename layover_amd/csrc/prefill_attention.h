@@ -310,7 +310,9 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 // could leave BF16's normal range is decoded exactly with the shift included (the reference's
 // decode_bits) and gets factor 1.
 struct PrefillStaged {
-    u32x4 w[4];  // BF16: 64 bytes; FP8: the first two hold 32 codes
+    // BF16: 64 bytes; FP8: w0 and w1 hold 32 codes. Named registers, not an array, so that the
+    // compiler keeps them in VGPRs (an indexed array here ended up in scratch memory).
+    u32x4 w0, w1, w2, w3;
     int32_t shift;
 };
 
@@ -376,37 +378,41 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
     const uint32_t row_bytes = part < 2 ? kLdsRowBytes : kLdsVRowBytes;
     const uint32_t lds_offset =
         (part < 2 ? part * kLdsTile : 2 * kLdsTile + (part - 2) * kLdsVTile) + (piece / 16) * row_bytes + (piece % 16) * 16;
-    auto load_step = [&](uint32_t step, PrefillStaged& r) {
+    auto load_step = [&](uint32_t step, PrefillStaged& r) __attribute__((always_inline)) {
         const uint32_t block_index = min(2 * step + (part & 1), last_block);
         const int32_t block = a.block_ids[block_index];
         const uint8_t* base = a.pool + uint64_t(uint32_t(block)) * a.block_bytes + part_offset;
         if constexpr (KV == LK_BF16) {
-#pragma unroll
-            for (int x = 0; x < 4; ++x) r.w[x] = *reinterpret_cast<const u32x4*>(base + 1024 * x);
+            r.w0 = *reinterpret_cast<const u32x4*>(base);
+            r.w1 = *reinterpret_cast<const u32x4*>(base + 1024);
+            r.w2 = *reinterpret_cast<const u32x4*>(base + 2048);
+            r.w3 = *reinterpret_cast<const u32x4*>(base + 3072);
         } else {
-#pragma unroll
-            for (int x = 0; x < 4; ++x) {
-                const u32x2 codes = *reinterpret_cast<const u32x2*>(base + 512 * x);
-                r.w[x / 2][2 * (x % 2)] = codes[0];
-                r.w[x / 2][2 * (x % 2) + 1] = codes[1];
-            }
+            const u32x2 c0 = *reinterpret_cast<const u32x2*>(base), c1 = *reinterpret_cast<const u32x2*>(base + 512);
+            const u32x2 c2 = *reinterpret_cast<const u32x2*>(base + 1024), c3 = *reinterpret_cast<const u32x2*>(base + 1536);
+            r.w0 = u32x4{c0[0], c0[1], c1[0], c1[1]};
+            r.w1 = u32x4{c2[0], c2[1], c3[0], c3[1]};
             r.shift = reinterpret_cast<const int16_t*>(a.pool + uint64_t(uint32_t(block)) * a.block_bytes + block_elems)[group];
         }
     };
-    auto store_step = [&](uint32_t buffer, const PrefillStaged& r) {
+    auto store_step = [&](uint32_t buffer, const PrefillStaged& r) __attribute__((always_inline)) {
         uint8_t* dst = lds[buffer] + lds_offset;
         if constexpr (KV == LK_BF16) {
-#pragma unroll
-            for (int x = 0; x < 4; ++x) *reinterpret_cast<u32x4*>(dst + 4 * row_bytes * x) = r.w[x];
+            *reinterpret_cast<u32x4*>(dst) = r.w0;
+            *reinterpret_cast<u32x4*>(dst + 4 * row_bytes) = r.w1;
+            *reinterpret_cast<u32x4*>(dst + 8 * row_bytes) = r.w2;
+            *reinterpret_cast<u32x4*>(dst + 12 * row_bytes) = r.w3;
         } else {
+            // Chunk x's 8 codes are words (2x, 2x + 1) of w0, w1.
             const bool exact = !shift_is_exact_in_fp32(r.shift);
-#pragma unroll
-            for (int x = 0; x < 4; ++x) {
-                const uint32_t lo = r.w[x / 2][2 * (x % 2)], hi = r.w[x / 2][2 * (x % 2) + 1];
-                *reinterpret_cast<u32x4*>(dst + 4 * row_bytes * x) =
-                    u32x4{fp8_pair(lo, false, exact, r.shift), fp8_pair(lo, true, exact, r.shift), fp8_pair(hi, false, exact, r.shift),
-                          fp8_pair(hi, true, exact, r.shift)};
-            }
+            auto convert = [&](uint32_t lo, uint32_t hi) __attribute__((always_inline)) {
+                return u32x4{fp8_pair(lo, false, exact, r.shift), fp8_pair(lo, true, exact, r.shift), fp8_pair(hi, false, exact, r.shift),
+                             fp8_pair(hi, true, exact, r.shift)};
+            };
+            *reinterpret_cast<u32x4*>(dst) = convert(r.w0[0], r.w0[1]);
+            *reinterpret_cast<u32x4*>(dst + 4 * row_bytes) = convert(r.w0[2], r.w0[3]);
+            *reinterpret_cast<u32x4*>(dst + 8 * row_bytes) = convert(r.w1[0], r.w1[1]);
+            *reinterpret_cast<u32x4*>(dst + 12 * row_bytes) = convert(r.w1[2], r.w1[3]);
             if (piece == 0) lds_shift[buffer][part] = r.shift;
         }
     };
@@ -431,7 +437,7 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
         float k[2];
         float v[2];
     };
-    auto factors = [&](uint32_t step) {
+    auto factors = [&](uint32_t step) __attribute__((always_inline)) {
         Factors f{{a.scale_log2, a.scale_log2}, {1.0f, 1.0f}};
         if constexpr (KV == LK_FP8_RECORD) {
 #pragma unroll
@@ -446,7 +452,7 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
 
     // K of a step as A operands (lane (g, n): key n, dims 32g + 8j .. +8), then one set's scores
     // S^T = K Q^T for both blocks.
-    auto read_k = [&](uint32_t step, bf16x8 (&kk)[2][4]) {
+    auto read_k = [&](uint32_t step, bf16x8 (&kk)[2][4]) __attribute__((always_inline)) {
         const uint8_t* buf = lds[step % kLdsBuffers];
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
@@ -455,7 +461,7 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
             for (int j = 0; j < 4; ++j) kk[b][j] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(k_row + 16 * j));
         }
     };
-    auto scores = [&](int set, const bf16x8 (&kk)[2][4], f32x4 (&s)[2]) {
+    auto scores = [&](int set, const bf16x8 (&kk)[2][4], f32x4 (&s)[2]) __attribute__((always_inline)) {
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -469,7 +475,7 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
 
     // V of a step as B operands, one per 16 output dims: keys 4g..4g+3 of block 0, then of
     // block 1, for dim 16e + n, as four BF16 pairs.
-    auto values = [&](uint32_t step, u32x4 (&vb)[8]) {
+    auto values = [&](uint32_t step, u32x4 (&vb)[8]) __attribute__((always_inline)) {
         const auto* buf = (const __attribute__((address_space(3))) uint8_t*)(lds[step % kLdsBuffers]);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -483,7 +489,7 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
 
     // Keys past a row's limit become -inf, for the maximum and the weight alike (exp2(-inf)
     // = 0: every live row sees key 0 in the first step, so m is finite).
-    auto mask = [&](uint32_t step, int set, f32x4 (&s)[2]) {
+    auto mask = [&](uint32_t step, int set, f32x4 (&s)[2]) __attribute__((always_inline)) {
         const uint32_t key0 = step * 2 * kSlots;
 #pragma unroll
         for (int b = 0; b < 2; ++b)
@@ -495,13 +501,13 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
     // Row maximum of one set's scores, taken on the raw scores of each block and then scaled
     // (the factors are positive). The state is rescaled only when a maximum grows by more than
     // kRescaleThreshold, which is rare after the first steps.
-    auto row_max = [&](const f32x4 (&s)[2], const Factors& f) {
+    auto row_max = [&](const f32x4 (&s)[2], const Factors& f) __attribute__((always_inline)) {
         float top_b[2];
 #pragma unroll
         for (int b = 0; b < 2; ++b) top_b[b] = fmaxf(fmaxf(fmaxf(s[b][0], s[b][1]), s[b][2]), s[b][3]) * f.k[b];
         return max_over_lane_groups(fmaxf(top_b[0], top_b[1]));
     };
-    auto rescale = [&](const float (&top)[2]) {
+    auto rescale = [&](const float (&top)[2]) __attribute__((always_inline)) {
         if (__builtin_expect(__any(top[0] > m[0] + kRescaleThreshold || top[1] > m[1] + kRescaleThreshold), 0)) {
             asm volatile("" ::: "memory");
 #pragma unroll
@@ -523,7 +529,7 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
 
     // One set's weights as a BF16 A operand (each exponent one FMA); FP8 pools weight each
     // block by its V factor and keep the unscaled sums per lane.
-    auto weights = [&](int set, const f32x4 (&s)[2], const Factors& f) {
+    auto weights = [&](int set, const f32x4 (&s)[2], const Factors& f) __attribute__((always_inline)) {
         float p[8];
 #pragma unroll
         for (int b = 0; b < 2; ++b)
@@ -541,7 +547,7 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
     };
 
     // One set's PV (and, for BF16 pools, its weight sums).
-    auto accumulate = [&](int set, const bf16x8& pb, const u32x4 (&vb)[8]) {
+    auto accumulate = [&](int set, const bf16x8& pb, const u32x4 (&vb)[8]) __attribute__((always_inline)) {
         if constexpr (KV == LK_BF16) sums[set] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pb, ones, sums[set], 0, 0, 0);
 #pragma unroll
         for (int e = 0; e < 8; ++e)
@@ -555,7 +561,7 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
     // that need the causal mask (and the chunk-end V mask, which only the last step can need)
     // run in a second copy of the loop. Forcing an MFMA/VALU interleave with scheduling
     // barriers measured 4% slower: the two waves on each SIMD already overlap each other.
-    auto run_step = [&](uint32_t step, auto masked_tag) {
+    auto run_step = [&](uint32_t step, auto masked_tag) __attribute__((always_inline)) {
         constexpr bool kMasked = decltype(masked_tag)::value;
         const Factors f = factors(step);
         bf16x8 kk[2][4];
