@@ -288,7 +288,9 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_mfma(PrefillArgs
 // and one computes while the other waits at its step barrier. Measured on MI355X at a
 // 2,048-token chunk ending a 32,768-token context: 2.97 ms per layer at one wave per SIMD and
 // 1.61 ms at two; 1.39 ms with conflict-free LDS stores, one FMA per weight's exponent, 32-bit
-// causal compares and permlane-swapped row maxima, with V regrouped by 32 v_perm per step.
+// causal compares and permlane-swapped row maxima, with V regrouped by 32 v_perm per step;
+// 1.18 ms with the transposing V reads, per-set stretches, masks only where needed and the
+// sums on the matrix cores.
 // O leaves through LDS: its rows are spread over lanes by dim (16e + n), so each wave writes
 // its 32 rows there and reads them back as 16-byte pieces of whole rows.
 constexpr uint32_t kLdsWaves = 4;
