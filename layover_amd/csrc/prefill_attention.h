@@ -500,23 +500,40 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
                 if (int32_t(key0 + b * kSlots + 4 * g + r) > limit[set]) s[b][r] = -INFINITY;
     };
 
-    // Row maximum of one set's scores, taken on the raw scores of each block and then scaled
-    // (the factors are positive). The state is rescaled only when a maximum grows by more than
-    // kRescaleThreshold, which is rare after the first steps.
-    auto row_max = [&](const f32x4 (&s)[2], const Factors& f) __attribute__((always_inline)) {
-        float top_b[2];
+    // Rescaling. The state of a row is rescaled only when a score exceeds its running maximum
+    // by more than kRescaleThreshold (log2 units), which is rare after the first steps. The
+    // common path therefore only compares each lane's own maximum with a precomputed limit:
+    // for BF16 pools on the raw scores against (m + threshold) / scale, for FP8 pools on the
+    // scaled scores of each block. Only when some lane exceeds it are the row maxima reduced
+    // over the lane groups (row n lives in lanes n, n + 16, n + 32, n + 48) and the state
+    // rescaled. A lane that misses the limit by rounding at most lets a weight reach 2^8 times
+    // an ulp more, which the threshold exists to bound anyway.
+    float raw_limit[2] = {-INFINITY, -INFINITY};  // BF16: (m + threshold) / scale per set
+    auto lane_max = [&](const f32x4 (&s)[2], const Factors& f) __attribute__((always_inline)) {
+        if constexpr (KV == LK_BF16) {
+            return fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])), fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+        } else {
+            float top_b[2];
 #pragma unroll
-        for (int b = 0; b < 2; ++b) top_b[b] = fmaxf(fmaxf(fmaxf(s[b][0], s[b][1]), s[b][2]), s[b][3]) * f.k[b];
-        return max_over_lane_groups(fmaxf(top_b[0], top_b[1]));
+            for (int b = 0; b < 2; ++b) top_b[b] = fmaxf(fmaxf(fmaxf(s[b][0], s[b][1]), s[b][2]), s[b][3]) * f.k[b];
+            return fmaxf(top_b[0], top_b[1]);
+        }
     };
-    auto rescale = [&](const float (&top)[2]) __attribute__((always_inline)) {
-        if (__builtin_expect(__any(top[0] > m[0] + kRescaleThreshold || top[1] > m[1] + kRescaleThreshold), 0)) {
+    auto exceeds = [&](int set, float lane_top) __attribute__((always_inline)) {
+        if constexpr (KV == LK_BF16) return lane_top > raw_limit[set];
+        else return lane_top > m[set] + kRescaleThreshold;
+    };
+    auto rescale = [&](const float (&lane_top)[2]) __attribute__((always_inline)) {
+        if (__builtin_expect(__any(exceeds(0, lane_top[0]) || exceeds(1, lane_top[1])), 0)) {
             asm volatile("" ::: "memory");
 #pragma unroll
             for (int set = 0; set < 2; ++set) {
-                const float next = top[set] > m[set] + kRescaleThreshold ? top[set] : m[set];
+                float top = max_over_lane_groups(lane_top[set]);
+                if constexpr (KV == LK_BF16) top *= a.scale_log2;
+                const float next = top > m[set] + kRescaleThreshold ? top : m[set];
                 const float alpha = merge_weight(m[set], next);
                 m[set] = next;
+                if constexpr (KV == LK_BF16) raw_limit[set] = (next + kRescaleThreshold) / a.scale_log2;
                 l[set] *= alpha;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
@@ -575,7 +592,7 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
         scores(1, kk, s[1]);
         if constexpr (kMasked) mask(step, 0, s[0]);
         float top[2];
-        top[0] = row_max(s[0], f);
+        top[0] = lane_max(s[0], f);
         if constexpr (kMasked) {
             mask(step, 1, s[1]);
             // Keys at or past the chunk's end hold anything: zero their V (0 * NaN is NaN).
@@ -595,7 +612,7 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
                 }
             }
         }
-        top[1] = row_max(s[1], f);
+        top[1] = lane_max(s[1], f);
         rescale(top);
         const bf16x8 p0 = weights(0, s[0], f);
         accumulate(0, p0, vb);
