@@ -609,55 +609,76 @@ __global__ __launch_bounds__(kWave) void decode_split_generic(DecodeArgs a) {
 
 template <int QF>
 __global__ __launch_bounds__(kWave) void decode_combine(DecodeArgs a, void* out) {
+    // Latency-bound at small batch (one wave per (sequence, query head), a few KiB each): every
+    // load that does not depend on another is issued at once. The sequence's length, the splits'
+    // (m, l) pairs and the first kChunk splits' rows all go out together; splits past the ones
+    // the sequence uses hold anything (the workspace is not initialized), so they are masked
+    // by selects, never multiplied by zero.
     const uint32_t lane = threadIdx.x;
     const uint32_t qh = blockIdx.x % a.query_heads;
     const uint32_t seq = blockIdx.x / a.query_heads;
-    const uint32_t used = (blocks_of(a.lengths[uint64_t(seq) * a.lengths_stride], a.slots) + a.bps - 1) / a.bps;
+    const int32_t length = a.lengths[uint64_t(seq) * a.lengths_stride];
     const uint64_t base = (uint64_t(seq) * a.query_heads + qh) * a.splits;
     const float* ml = a.partial_ml + 2 * base;
+    const float* acc = a.partial_acc + base * a.head_dim;
+    constexpr uint32_t kPer = kMaxGenericDim / kWave;
+    constexpr uint32_t kChunk = 16;
+    // Lane s holds split s's (m, l) for the first kWave splits (more only beyond 64 splits).
+    float lane_m = -INFINITY, lane_l = 0.0f;
+    if (lane < a.splits) {
+        lane_m = ml[2 * lane];
+        lane_l = ml[2 * lane + 1];
+    }
+    auto load_rows = [&](uint32_t chunk, float (&rows)[kChunk][kPer]) {
+#pragma unroll
+        for (uint32_t u = 0; u < kChunk; ++u) {
+            const float* row = acc + uint64_t(min(chunk + u, a.splits - 1)) * a.head_dim;
+#pragma unroll
+            for (uint32_t i = 0; i < kPer; ++i) {
+                const uint32_t d = lane + i * kWave;
+                rows[u][i] = d < a.head_dim ? row[d] : 0.0f;
+            }
+        }
+    };
+    float rows[kChunk][kPer];
+    load_rows(0, rows);
 
-    // Lanes across splits: the largest running max, then the total weight.
-    float top = -INFINITY;
-    for (uint32_t s = lane; s < used; s += kWave) top = fmaxf(top, ml[2 * s]);
+    const uint32_t used = (blocks_of(length, a.slots) + a.bps - 1) / a.bps;
+    // The largest running max over the used splits, then the total weight.
+    float top = lane < used ? lane_m : -INFINITY;
+    for (uint32_t s = lane + kWave; s < used; s += kWave) top = fmaxf(top, ml[2 * s]);
 #pragma unroll
     for (int mask = 32; mask >= 1; mask >>= 1) top = fmaxf(top, __shfl_xor(top, mask, kWave));
-    float total = 0.0f;
-    for (uint32_t s = lane; s < used; s += kWave) total += ml[2 * s + 1] * merge_weight(ml[2 * s], top);
+    float total = lane < used ? lane_l * merge_weight(lane_m, top) : 0.0f;
+    for (uint32_t s = lane + kWave; s < used; s += kWave) total += ml[2 * s + 1] * merge_weight(ml[2 * s], top);
 #pragma unroll
     for (int mask = 32; mask >= 1; mask >>= 1) total += __shfl_xor(total, mask, kWave);
     const float inverse = 1.0f / total;
 
-    // Lanes across dims: sum the splits' accumulators, 64 splits' weights at a time, each
-    // broadcast from the lane that computed it. Rows are read eight at a time, so eight loads
-    // are in flight per lane instead of one round trip per split.
-    constexpr uint32_t kPer = kMaxGenericDim / kWave;
-    constexpr uint32_t kBatch = 8;
+    // Lanes across dims: sum the used splits' accumulators, each split's weight broadcast from
+    // the lane that holds its (m, l); the next chunk's rows are loaded before this one is summed.
     float sum[kPer];
 #pragma unroll
     for (uint32_t i = 0; i < kPer; ++i) sum[i] = 0.0f;
-    const float* acc = a.partial_acc + base * a.head_dim;
-    for (uint32_t chunk = 0; chunk < used; chunk += kWave) {
-        const uint32_t s = chunk + lane;
-        const float weight = s < used ? merge_weight(ml[2 * s], top) : 0.0f;
-        const uint32_t n = min(kWave, used - chunk);
-        for (uint32_t j0 = 0; j0 < n; j0 += kBatch) {
-            float rows[kBatch][kPer];
+    for (uint32_t chunk = 0; chunk < used; chunk += kChunk) {
+        float next[kChunk][kPer];
+        const bool more = chunk + kChunk < used;
+        if (more) load_rows(chunk + kChunk, next);
+        const uint32_t window = chunk & ~(kWave - 1);  // the 64 splits whose (m, l) lanes hold
+        const float weight_lane = window == 0 ? (lane < used ? merge_weight(lane_m, top) : 0.0f)
+                                              : (window + lane < used ? merge_weight(ml[2 * (window + lane)], top) : 0.0f);
 #pragma unroll
-            for (uint32_t u = 0; u < kBatch; ++u) {
-                // Past the last split, re-read it with weight zero rather than branch.
-                const float* row = acc + uint64_t(chunk + min(j0 + u, n - 1)) * a.head_dim;
+        for (uint32_t u = 0; u < kChunk; ++u) {
+            const uint32_t s = chunk + u;
+            const float w = __shfl(weight_lane, int((s - window) % kWave), kWave);
 #pragma unroll
-                for (uint32_t i = 0; i < kPer; ++i) {
-                    const uint32_t d = lane + i * kWave;
-                    rows[u][i] = d < a.head_dim ? row[d] : 0.0f;
-                }
-            }
+            for (uint32_t i = 0; i < kPer; ++i) sum[i] = s < used ? fmaf(w, rows[u][i], sum[i]) : sum[i];
+        }
+        if (more) {
 #pragma unroll
-            for (uint32_t u = 0; u < kBatch; ++u) {
-                const float w = __shfl(weight, int(min(j0 + u, kWave - 1)), kWave) * (j0 + u < n ? 1.0f : 0.0f);
+            for (uint32_t u = 0; u < kChunk; ++u)
 #pragma unroll
-                for (uint32_t i = 0; i < kPer; ++i) sum[i] = fmaf(w, rows[u][i], sum[i]);
-            }
+                for (uint32_t i = 0; i < kPer; ++i) rows[u][i] = next[u][i];
         }
     }
 #pragma unroll
