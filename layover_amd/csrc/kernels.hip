@@ -517,65 +517,176 @@ LK_EXPORT int lk_paged_decode(const lk_decode_shape* shape, const void* q, const
     });
 }
 
+namespace lk {
+
+// Split-K plan for the LDS prefill kernel. Workgroups are (KV head, 128-row tile); a chunk
+// whose tiles do not give every CU two of them (short chunks against long histories) also
+// splits each tile's keys, at least 4 steps (128 keys) per split and at most kMaxKeySplits
+// splits, and merges the partials in prefill_merge. LAYOVER_PREFILL_SPLITS=n forces n
+// splits (tests), read per launch.
+struct PrefillPlan {
+    uint64_t row_tiles;
+    uint32_t key_splits;
+    uint32_t split_steps;
+    bool shared;  // the LDS kernel (the register-only one never splits)
+};
+
+// CUs of the current device, cached per device; 256 (MI355X) when no device answers, with the
+// failed query's error cleared so that it is not reported by a later check.
+uint32_t compute_units() {
+    static int units[64] = {};
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) {
+        (void)hipGetLastError();
+        return 256;
+    }
+    if (units[device] == 0) {
+        int count = 0;
+        if (hipDeviceGetAttribute(&count, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || count <= 0) {
+            (void)hipGetLastError();
+            return 256;
+        }
+        units[device] = count;
+    }
+    return uint32_t(units[device]);
+}
+
+PrefillPlan prefill_plan(const lk_prefill_shape& s) {
+    PrefillPlan p{};
+    const uint32_t groups = s.query_heads / s.kv_heads;
+    const uint64_t rows = uint64_t(s.tokens) * groups;
+    // The LDS-shared kernel (128 rows a workgroup) unless LAYOVER_PREFILL_KERNEL=1 asks for the
+    // register-only one (64 rows a workgroup, each wave streaming its own tiles).
+    const char* choice = getenv("LAYOVER_PREFILL_KERNEL");
+    p.shared = !(choice && strtoul(choice, nullptr, 10) == 1);
+    const uint64_t tile_rows = p.shared ? uint64_t(kLdsRows) * kLdsWaves : uint64_t(kPrefillRows) * kPrefillWaves;
+    p.row_tiles = (rows + tile_rows - 1) / tile_rows;
+    const uint64_t end = uint64_t(s.start) + s.tokens;
+    const uint32_t max_steps = uint32_t((((end + kSlots - 1) / kSlots) + 1) / 2);
+    p.key_splits = 1;
+    p.split_steps = max_steps;
+    if (!p.shared) return p;
+    uint32_t wanted = 0;
+    if (const char* forced = getenv("LAYOVER_PREFILL_SPLITS")) {
+        wanted = uint32_t(strtoul(forced, nullptr, 10));
+    } else {
+        const uint64_t workgroups = p.row_tiles * s.kv_heads, target = 2ull * compute_units();
+        if (workgroups < target) {
+            const uint64_t fill = (target + workgroups - 1) / workgroups, cap = max_steps / 4;
+            wanted = uint32_t(fill < cap ? fill : cap);
+        }
+    }
+    const uint32_t most = kMaxKeySplits < max_steps ? kMaxKeySplits : max_steps;
+    wanted = wanted < 1 ? 1 : (wanted > most ? most : wanted);
+    if (wanted <= 1) return p;
+    p.split_steps = (max_steps + wanted - 1) / wanted;
+    p.key_splits = (max_steps + p.split_steps - 1) / p.split_steps;
+    return p;
+}
+
+uint64_t prefill_workspace(const lk_prefill_shape& s, const PrefillPlan& p) {
+    if (p.key_splits <= 1) return 0;
+    const uint64_t rows = uint64_t(s.tokens) * (s.query_heads / s.kv_heads);
+    return uint64_t(s.kv_heads) * rows * p.key_splits * (kDim + 2) * sizeof(float);
+}
+
+void check_prefill(const lk_prefill_shape& s) {
+    require(s.tokens > 0 && s.query_heads > 0 && s.kv_heads > 0 && s.layers > 0, "every prefill dimension must be positive");
+    require(s.query_heads % s.kv_heads == 0, "query heads must be a multiple of KV heads");
+    require(s.layer < s.layers, "layer out of range");
+    require(s.slots == kSlots && s.head_dim == kDim, "paged prefill supports 16-slot blocks of 128 dims");
+    require(s.q_format == LK_BF16, "paged prefill takes BF16 q");
+    require(s.kv_format == LK_BF16 || s.kv_format == LK_FP8_RECORD, "paged prefill reads BF16 or FP8-record pools");
+    require(uint64_t(s.start) + s.tokens <= 0x7FFFFFFFull, "a chunk must end below 2^31 tokens");
+}
+
+void run_prefill(const lk_prefill_shape& s, const void* q, const void* pool, const int32_t* block_ids, uint32_t num_block_ids, void* out,
+                 void* workspace, uint64_t workspace_bytes, bool may_split, hipStream_t st) {
+    require(q && pool && block_ids && out, "null q, pool, block ids or out");
+    check_prefill(s);
+    const uint64_t end = uint64_t(s.start) + s.tokens;
+    require(uint64_t(num_block_ids) * s.slots >= end, "fewer block ids than the chunk's end needs");
+    lk_decode_shape d{};
+    d.layers = s.layers;
+    d.kv_heads = s.kv_heads;
+    d.slots = s.slots;
+    d.head_dim = s.head_dim;
+    d.kv_format = s.kv_format;
+    const uint64_t block_bytes = pool_block_bytes(d);
+    require(aligned(q, 16) && aligned(out, 16) && aligned(pool, 16) && block_bytes % 16 == 0, "q, out and pool blocks must be 16-byte aligned");
+    PrefillPlan p = prefill_plan(s);
+    if (!may_split) {
+        p.key_splits = 1;
+        p.split_steps = uint32_t((((end + kSlots - 1) / kSlots) + 1) / 2);
+    }
+    const uint64_t need = prefill_workspace(s, p);
+    require(need == 0 || (workspace != nullptr && workspace_bytes >= need && aligned(workspace, 4)),
+            "workspace smaller than lk_paged_prefill_workspace");
+    const uint32_t groups = s.query_heads / s.kv_heads;
+    const uint64_t rows = uint64_t(s.tokens) * groups;
+    const uint64_t grid = p.row_tiles * s.kv_heads * p.key_splits;
+    require(rows <= 0xFFFFFFFFull && grid <= 0x7FFFFFFFull, "prefill chunk too large for one launch");
+    PrefillArgs a{};
+    a.q = static_cast<const uint16_t*>(q);
+    a.pool = static_cast<const uint8_t*>(pool);
+    a.block_ids = block_ids;
+    a.out = static_cast<uint16_t*>(out);
+    a.tokens = s.tokens;
+    a.start = s.start;
+    a.query_heads = s.query_heads;
+    a.kv_heads = s.kv_heads;
+    a.groups = groups;
+    a.layers = s.layers;
+    a.layer = s.layer;
+    a.row_tiles = uint32_t(p.row_tiles);
+    a.block_bytes = block_bytes;
+    a.scale_log2 = s.scale * kLog2e;
+    a.key_splits = p.key_splits;
+    a.split_steps = p.split_steps;
+    a.partial_acc = static_cast<float*>(workspace);
+    a.partial_ml = p.key_splits > 1 ? a.partial_acc + uint64_t(s.kv_heads) * rows * p.key_splits * kDim : nullptr;
+    if (p.shared && s.kv_format == LK_BF16)
+        hipLaunchKernelGGL(prefill_mfma_lds<LK_BF16>, dim3(uint32_t(grid)), dim3(kWave * kLdsWaves), 0, st, a);
+    else if (p.shared)
+        hipLaunchKernelGGL(prefill_mfma_lds<LK_FP8_RECORD>, dim3(uint32_t(grid)), dim3(kWave * kLdsWaves), 0, st, a);
+    else if (s.kv_format == LK_BF16)
+        hipLaunchKernelGGL(prefill_mfma<LK_BF16>, dim3(uint32_t(grid)), dim3(kWave * kPrefillWaves), 0, st, a);
+    else
+        hipLaunchKernelGGL(prefill_mfma<LK_FP8_RECORD>, dim3(uint32_t(grid)), dim3(kWave * kPrefillWaves), 0, st, a);
+    if (p.key_splits > 1) {
+        const uint64_t units = uint64_t(s.kv_heads) * rows;
+        hipLaunchKernelGGL(prefill_merge, dim3(uint32_t((units + 3) / 4)), dim3(kWave * 4), 0, st, a);
+    }
+}
+
+}  // namespace lk
+
 LK_EXPORT int lk_paged_prefill(const lk_prefill_shape* shape, const void* q, const void* pool, const int32_t* block_ids,
                                uint32_t num_block_ids, void* out, void* stream) {
     return lk::guarded([&] {
         lk::require(shape != nullptr, "null shape");
-        const lk_prefill_shape& s = *shape;
-        lk::require(q && pool && block_ids && out, "null q, pool, block ids or out");
-        lk::require(s.tokens > 0 && s.query_heads > 0 && s.kv_heads > 0 && s.layers > 0, "every prefill dimension must be positive");
-        lk::require(s.query_heads % s.kv_heads == 0, "query heads must be a multiple of KV heads");
-        lk::require(s.layer < s.layers, "layer out of range");
-        lk::require(s.slots == lk::kSlots && s.head_dim == lk::kDim, "paged prefill supports 16-slot blocks of 128 dims");
-        lk::require(s.q_format == LK_BF16, "paged prefill takes BF16 q");
-        lk::require(s.kv_format == LK_BF16 || s.kv_format == LK_FP8_RECORD, "paged prefill reads BF16 or FP8-record pools");
-        const uint64_t end = uint64_t(s.start) + s.tokens;
-        lk::require(uint64_t(num_block_ids) * s.slots >= end, "fewer block ids than the chunk's end needs");
-        lk::require(end <= 0x7FFFFFFFull, "a chunk must end below 2^31 tokens");
-        lk_decode_shape d{};
-        d.layers = s.layers;
-        d.kv_heads = s.kv_heads;
-        d.slots = s.slots;
-        d.head_dim = s.head_dim;
-        d.kv_format = s.kv_format;
-        const uint64_t block_bytes = lk::pool_block_bytes(d);
-        lk::require(lk::aligned(q, 16) && lk::aligned(out, 16) && lk::aligned(pool, 16) && block_bytes % 16 == 0,
-                    "q, out and pool blocks must be 16-byte aligned");
-        const uint32_t groups = s.query_heads / s.kv_heads;
-        const uint64_t rows = uint64_t(s.tokens) * groups;
-        // The LDS-shared kernel (128 rows a workgroup) unless LAYOVER_PREFILL_KERNEL=1 asks for
-        // the register-only one (64 rows a workgroup, each wave streaming its own tiles).
-        const char* choice = getenv("LAYOVER_PREFILL_KERNEL");
-        const bool register_only = choice && strtoul(choice, nullptr, 10) == 1;
-        const bool shared = !register_only;
-        const uint64_t tile_rows = shared ? uint64_t(lk::kLdsRows) * lk::kLdsWaves : uint64_t(lk::kPrefillRows) * lk::kPrefillWaves;
-        const uint64_t row_tiles = (rows + tile_rows - 1) / tile_rows;
-        const uint64_t grid = row_tiles * s.kv_heads;
-        lk::require(rows <= 0xFFFFFFFFull && grid <= 0x7FFFFFFFull, "prefill chunk too large for one launch");
-        lk::PrefillArgs a{};
-        a.q = static_cast<const uint16_t*>(q);
-        a.pool = static_cast<const uint8_t*>(pool);
-        a.block_ids = block_ids;
-        a.out = static_cast<uint16_t*>(out);
-        a.tokens = s.tokens;
-        a.start = s.start;
-        a.query_heads = s.query_heads;
-        a.kv_heads = s.kv_heads;
-        a.groups = groups;
-        a.layers = s.layers;
-        a.layer = s.layer;
-        a.row_tiles = uint32_t(row_tiles);
-        a.block_bytes = block_bytes;
-        a.scale_log2 = s.scale * lk::kLog2e;
-        auto st = static_cast<hipStream_t>(stream);
-        if (shared && s.kv_format == LK_BF16)
-            hipLaunchKernelGGL(lk::prefill_mfma_lds<LK_BF16>, dim3(uint32_t(grid)), dim3(lk::kWave * lk::kLdsWaves), 0, st, a);
-        else if (shared)
-            hipLaunchKernelGGL(lk::prefill_mfma_lds<LK_FP8_RECORD>, dim3(uint32_t(grid)), dim3(lk::kWave * lk::kLdsWaves), 0, st, a);
-        else if (s.kv_format == LK_BF16)
-            hipLaunchKernelGGL(lk::prefill_mfma<LK_BF16>, dim3(uint32_t(grid)), dim3(lk::kWave * lk::kPrefillWaves), 0, st, a);
-        else
-            hipLaunchKernelGGL(lk::prefill_mfma<LK_FP8_RECORD>, dim3(uint32_t(grid)), dim3(lk::kWave * lk::kPrefillWaves), 0, st, a);
+        lk::run_prefill(*shape, q, pool, block_ids, num_block_ids, out, nullptr, 0, false, static_cast<hipStream_t>(stream));
+    });
+}
+
+LK_EXPORT uint64_t lk_paged_prefill_workspace(const lk_prefill_shape* shape) {
+    // No launch here, so no HIP error check either (without a device every HIP call reports
+    // one; the plan then assumes 256 CUs).
+    if (shape == nullptr) return 0;
+    try {
+        lk::check_prefill(*shape);
+        return lk::prefill_workspace(*shape, lk::prefill_plan(*shape));
+    } catch (const std::exception& error) {
+        lk::last_error = error.what();
+        return 0;
+    }
+}
+
+LK_EXPORT int lk_paged_prefill_split(const lk_prefill_shape* shape, const void* q, const void* pool, const int32_t* block_ids,
+                                     uint32_t num_block_ids, void* out, void* workspace, uint64_t workspace_bytes, void* stream) {
+    return lk::guarded([&] {
+        lk::require(shape != nullptr, "null shape");
+        lk::run_prefill(*shape, q, pool, block_ids, num_block_ids, out, workspace, workspace_bytes, true, static_cast<hipStream_t>(stream));
     });
 }
 

@@ -38,7 +38,20 @@ struct PrefillArgs {
     uint32_t row_tiles;        // workgroups per KV head
     uint64_t block_bytes;
     float scale_log2;
+    // Split-K (the LDS kernel only): workgroup (KV head, row tile, split) takes key steps
+    // [split * split_steps, (split + 1) * split_steps) of its tile and, with key_splits > 1,
+    // writes unnormalized partials [kv_heads, rows, key_splits] of (acc[128]) and (m, l)
+    // instead of out; prefill_merge then combines them.
+    uint32_t key_splits;       // 1: no split, results straight to out
+    uint32_t split_steps;
+    float* partial_acc;
+    float* partial_ml;
 };
+
+// The running maximum of a row that has seen no key yet: finite, so that a weight taken
+// against it is exp2(-inf) = 0 even when every score of the step is masked (a split can hold
+// no visible key for some of its rows), and its merge weight exp2(kNoMax - m) underflows to 0.
+constexpr float kNoMax = -1e30f;
 
 template <int KV>
 __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_mfma(PrefillArgs a) {
@@ -326,8 +339,11 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const uint32_t g = lane / 16;
     const uint32_t n = lane % 16;
+    // KV head fastest (a head's workgroups stay on one XCD), then the splits of a tile, then
+    // the tiles, heaviest first.
     const uint32_t kv_head = blockIdx.x % a.kv_heads;
-    const uint32_t tile = a.row_tiles - 1 - blockIdx.x / a.kv_heads;
+    const uint32_t split = (blockIdx.x / a.kv_heads) % a.key_splits;
+    const uint32_t tile = a.row_tiles - 1 - blockIdx.x / (a.kv_heads * a.key_splits);
     const uint32_t total_rows = a.tokens * a.groups;
     const uint32_t wg_row0 = tile * kLdsWaves * kLdsRows;
     const uint32_t row0 = wg_row0 + wave * kLdsRows;
@@ -336,7 +352,10 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
     // Keys the workgroup needs: up to its last row's limit; in steps of two blocks.
     const uint32_t wg_last = min(wg_row0 + kLdsWaves * kLdsRows, total_rows) - 1;
     const uint32_t key_blocks = (a.start + wg_last / a.groups) / kSlots + 1;
-    const uint32_t steps = (key_blocks + 1) / 2;
+    const uint32_t tile_steps = (key_blocks + 1) / 2;
+    // This workgroup's steps [first_step, steps); a split past the tile's keys does none.
+    const uint32_t first_step = min(split * a.split_steps, tile_steps);
+    const uint32_t steps = min(first_step + a.split_steps, tile_steps);
     const uint32_t last_block = (end + kSlots - 1) / kSlots - 1;
     // The wave's first row's limit (later rows only see more keys); -1 for a wave past the end.
     const int64_t first_limit = row0 < total_rows ? int64_t(a.start) + row0 / a.groups : -1;
@@ -421,7 +440,7 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
 
     // Running maximum per row (lane (g, n): row n of each set); output and, for BF16 pools,
     // weight sums in the MFMA output layout (lane (g, n): rows 4g + r, dims 16e + n).
-    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
+    float m[2] = {kNoMax, kNoMax}, l[2] = {0.0f, 0.0f};
     f32x4 o[2][8], sums[2];
 #pragma unroll
     for (int set = 0; set < 2; ++set) {
@@ -625,15 +644,48 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
         __syncthreads();
     };
 
-    load_step(0, staged);
-    store_step(0, staged);
-    if (steps > 1) load_step(1, staged);
-    __syncthreads();
-    // Steps whose 32 keys all lie at or below the wave's first row's limit need no mask.
-    const uint32_t unmasked = first_limit < 0 ? 0u : min(steps, uint32_t((first_limit + 1) / (2 * kSlots)));
-    uint32_t step = 0;
-    for (; step < unmasked; ++step) run_step(step, std::false_type{});
-    for (; step < steps; ++step) run_step(step, std::true_type{});
+    if (first_step < steps) {
+        load_step(first_step, staged);
+        store_step(first_step % kLdsBuffers, staged);
+        if (first_step + 1 < steps) load_step(first_step + 1, staged);
+        __syncthreads();
+        // Steps whose 32 keys all lie at or below the wave's first row's limit need no mask.
+        const uint32_t unmasked = first_limit < 0 ? 0u : min(steps, uint32_t((first_limit + 1) / (2 * kSlots)));
+        uint32_t step = first_step;
+        for (; step < unmasked; ++step) run_step(step, std::false_type{});
+        for (; step < steps; ++step) run_step(step, std::true_type{});
+    }
+
+    if (a.key_splits > 1) {
+        // Unnormalized partials of this split: lane (g, n) holds rows 4g + r of each set (dims
+        // 16e + n); the row's running maximum lives in lane 4g + r (row n of the score layout).
+#pragma unroll
+        for (int set = 0; set < 2; ++set) {
+            float row_l;
+            if constexpr (KV == LK_BF16) {
+                row_l = 0.0f;
+            } else {
+                row_l = l[set];
+                row_l += __shfl_xor(row_l, 16, kWave);
+                row_l += __shfl_xor(row_l, 32, kWave);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float row_m = __shfl(m[set], int(4 * g + r), kWave);
+                const float total = KV == LK_BF16 ? sums[set][r] : __shfl(row_l, int(4 * g + r), kWave);
+                const uint32_t row = row0 + 16 * set + 4 * g + r;
+                if (row >= total_rows) continue;
+                const uint64_t slot = (uint64_t(kv_head) * total_rows + row) * a.key_splits + split;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) a.partial_acc[slot * kDim + 16 * e + n] = o[set][e][r];
+                if (n == 0) {
+                    a.partial_ml[2 * slot] = row_m;
+                    a.partial_ml[2 * slot + 1] = total;
+                }
+            }
+        }
+        return;
+    }
 
     // Row totals in the layout of O: lane (g, n) needs rows 4g + r. FP8 pools summed per lane
     // (row n, a quarter of the keys each): reduce over the lane groups, then fetch row 4g + r.
@@ -677,6 +729,41 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
                 *reinterpret_cast<const u32x4*>(staging + local_row * kLdsRowBytes + 16 * (piece_index % 16));
         }
     }
+}
+
+
+// Split-K merge: one wave per (KV head, row), 4 rows a workgroup; lane s holds split s's
+// (m, l) (at most 64 splits), lanes across dims sum the splits' accumulators in split order.
+constexpr uint32_t kMaxKeySplits = 64;
+
+__global__ __launch_bounds__(kWave * 4) void prefill_merge(PrefillArgs a) {
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint32_t total_rows = a.tokens * a.groups;
+    const uint64_t unit = uint64_t(blockIdx.x) * 4 + threadIdx.x / kWave;  // kv_head * rows + row
+    if (unit >= uint64_t(a.kv_heads) * total_rows) return;
+    const uint32_t kv_head = uint32_t(unit / total_rows), row = uint32_t(unit % total_rows);
+    const uint64_t base = unit * a.key_splits;
+    const float lane_m = lane < a.key_splits ? a.partial_ml[2 * (base + lane)] : kNoMax;
+    const float lane_l = lane < a.key_splits ? a.partial_ml[2 * (base + lane) + 1] : 0.0f;
+    float top = lane_m;
+#pragma unroll
+    for (int mask = 32; mask >= 1; mask >>= 1) top = fmaxf(top, __shfl_xor(top, mask, kWave));
+    const float weight = exp2_fast(lane_m - top);  // kNoMax splits: exp2(-1e30) = 0
+    float total = lane_l * weight;
+#pragma unroll
+    for (int mask = 32; mask >= 1; mask >>= 1) total += __shfl_xor(total, mask, kWave);
+    const float inverse = 1.0f / total;
+    float sum[2] = {0.0f, 0.0f};
+    for (uint32_t s = 0; s < a.key_splits; ++s) {
+        const float w = __shfl(weight, int(s), kWave);
+        const float* acc = a.partial_acc + (base + s) * kDim;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) sum[i] = fmaf(w, acc[lane + kWave * i], sum[i]);
+    }
+    const uint32_t token = row / a.groups, head = kv_head * a.groups + row % a.groups;
+    uint16_t* out = a.out + (uint64_t(head) * a.tokens + token) * kDim;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) out[lane + kWave * i] = to_bf16(sum[i] * inverse);
 }
 
 }  // namespace lk

@@ -53,16 +53,20 @@ def validate(q, pool, layer: int, block_ids: torch.Tensor, start: int, kv_groups
 def run_kernel(q, pool, layer: int, block_ids: torch.Tensor, start: int, kv_groups: int, out: torch.Tensor) -> None:
     """Launch on the current stream into `out` (q's shape and dtype). Block ids are not read
     on the host: the caller has checked them against the pool (as chunk_locations' table
-    does)."""
+    does). A chunk whose tiles would leave CUs idle splits its keys (split-K) into a workspace
+    taken from torch's allocator on this stream, then merges them."""
     query_heads, tokens, head_dim = q.shape
     _, _, layers, kv_heads, slots, _ = pool.shape
     kv_format = _lib.LK_FP8_RECORD if _is_fp8(pool) else _lib.LK_BF16
     shape = _lib.PrefillShape(tokens, start, query_heads, kv_heads, head_dim, layers, slots, layer, _lib.LK_BF16, kv_format,
                               1.0 / math.sqrt(head_dim))
     storage = pool.records if isinstance(pool, Fp8KVPool) else pool
+    lib = _lib.load()
+    need = int(lib.lk_paged_prefill_workspace(shape))
+    workspace = torch.empty(need, dtype=torch.uint8, device=q.device) if need else None
     _lib.check(
-        _lib.load().lk_paged_prefill(shape, q.data_ptr(), storage.data_ptr(), block_ids.data_ptr(), block_ids.shape[0], out.data_ptr(),
-                                     _lib.current_stream(q.device))
+        lib.lk_paged_prefill_split(shape, q.data_ptr(), storage.data_ptr(), block_ids.data_ptr(), block_ids.shape[0], out.data_ptr(),
+                                   workspace.data_ptr() if need else None, need, _lib.current_stream(q.device))
     )
 
 

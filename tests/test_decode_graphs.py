@@ -147,3 +147,22 @@ def test_token_write_and_prefill_arguments_are_checked_without_a_gpu():
         hip_prefill.paged_prefill_attention_hip(q[..., :64].contiguous(), pool[..., :64].contiguous(), 0, ids, 0, 4)
     with pytest.raises(ValueError, match="cannot hold"):
         hip_prefill.paged_prefill_attention_hip(q, pool, 0, ids[:1], 10, 4)
+
+
+def test_prefill_split_plan_sizes_its_workspace(monkeypatch):
+    """Short chunks against long histories split their keys; full-GPU chunks do not. The plan
+    assumes 256 CUs when no device answers (as here)."""
+    from layover_amd.kernels import _lib
+
+    lib = _lib.load()
+    long_chunk = _lib.PrefillShape(2048, 30720, 32, 8, 128, 36, 16, 0, _lib.LK_BF16, _lib.LK_BF16, 128**-0.5)
+    assert lib.lk_paged_prefill_workspace(long_chunk) == 0  # 16 x 8 x 4 = 512 workgroups fill 256 CUs twice
+    short = _lib.PrefillShape(512, 8192, 32, 8, 128, 36, 16, 0, _lib.LK_BF16, _lib.LK_BF16, 128**-0.5)
+    # 128 workgroups: 4 splits of 68 of the 272 key steps; partials [8, 2048 rows, 4] x (128 + 2) floats.
+    assert lib.lk_paged_prefill_workspace(short) == 8 * 2048 * 4 * 130 * 4
+    monkeypatch.setenv("LAYOVER_PREFILL_SPLITS", "1")
+    assert lib.lk_paged_prefill_workspace(short) == 0
+    monkeypatch.setenv("LAYOVER_PREFILL_SPLITS", "1000")  # capped at 64: 5 steps each, so 55 splits
+    assert lib.lk_paged_prefill_workspace(short) == 8 * 2048 * 55 * 130 * 4
+    bad = _lib.PrefillShape(512, 8192, 30, 8, 128, 36, 16, 0, _lib.LK_BF16, _lib.LK_BF16, 1.0)
+    assert lib.lk_paged_prefill_workspace(bad) == 0

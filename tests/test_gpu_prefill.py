@@ -161,3 +161,24 @@ def test_prefill_fp8_tiny_groups_take_the_exact_decode(kernel, monkeypatch):
     torch.cuda.synchronize()
     reference = oracle.prefill_attention(q.float().cpu().numpy(), state, 1, block_ids, 50, 4)
     assert_close(out.float() * 2.0**114, reference * 2.0**114)
+
+
+@pytest.mark.parametrize("splits", ["1", "3", "7"])
+@pytest.mark.parametrize("fp8", [False, True], ids=["bf16_pool", "fp8_pool"])
+@pytest.mark.parametrize("start,tokens", [(0, 37), (1000, 130), (4090, 7), (300, 90)])
+def test_split_keys_match_the_oracle(start, tokens, fp8, splits, monkeypatch):
+    """Split-K: each tile's key steps spread over 1, 3 or 7 workgroups whose partials are
+    merged. Splits that hold no visible key for some rows (or none at all) must contribute
+    nothing, not NaN."""
+    from layover_amd.kernels.hip_prefill import paged_prefill_attention_hip
+
+    monkeypatch.setenv("LAYOVER_PREFILL_SPLITS", splits)
+    end = start + tokens
+    blocks = -(-end // 16)
+    pool, state = make_pool(blocks, 2, 8, seed=tokens, fp8=fp8)
+    block_ids = np.random.default_rng(start).permutation(blocks).astype(np.int32)
+    q = torch.randn(32, tokens, 128, device="cuda").to(torch.bfloat16)
+    print(f"prefill split={splits} fp8={fp8} start={start} tokens={tokens}", flush=True)
+    out = paged_prefill_attention_hip(q, pool, 1, torch.from_numpy(block_ids).cuda(), start, 4)
+    torch.cuda.synchronize()
+    assert_close(out, oracle.prefill_attention(q.float().cpu().numpy(), state, 1, block_ids, start, 4))
