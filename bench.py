@@ -384,7 +384,7 @@ def prefill_bench(device, layers: int = 36) -> list:
     from layover_amd.kernels.hip_prefill import paged_prefill_attention_hip
 
     runs = []
-    for start, tokens in ((0, 2048), (30720, 2048)):
+    for start, tokens in ((0, 2048), (30720, 2048), (8192, 512)):
         end = start + tokens
         blocks = -(-end // 16)
         pool = torch.empty(blocks + 1, 2, layers, QWEN["kv_heads"], 16, QWEN["head_dim"], dtype=torch.bfloat16, device=device)
