@@ -374,8 +374,9 @@ def graph_decode_bench(device, cache, fp8_pool, steps: int = 20) -> list:
 
 
 def prefill_bench(device, layers: int = 36) -> list:
-    """Paged causal prefill of one 2,048-token chunk (Qwen3-4B heads), per layer: the chunk
-    at the start of a sequence and at the end of a 32,768-token context. Beside it, the
+    """Paged causal prefill (Qwen3-4B heads), per layer: a 2,048-token chunk at the start of a
+    sequence and at the end of a 32,768-token context, and a 512-token chunk at position 8,192
+    (too few row tiles to fill the GPU, so its keys are split). Beside it, the
     reference's GPU path on this GPU (model.py:69-98): gather the history out of the pool,
     then torch's flash attention with the bottom-right causal mask. FLOPs count the causal
     score and value products: 4 x head_dim x visible keys per query row."""
