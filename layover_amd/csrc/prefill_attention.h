@@ -275,9 +275,9 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_mfma(PrefillArgs
 // ---------------------------------------------------------------------------------------
 // K/V shared through LDS. A workgroup of 4 waves owns 128 rows (32 per wave, as two sets of
 // 16) and walks the keys in steps of 32 (two blocks). Each step's K and V tiles (4 x 4 KiB)
-// are loaded once per workgroup, every thread bringing 64 contiguous bytes, into one of two
-// LDS buffers while the other is read; the next step's bytes are already in registers, loaded
-// one step ahead. Per wave and step:
+// are loaded once per workgroup: for BF16 pools by direct-to-LDS copies two steps ahead into
+// one of three buffers, for FP8 pools through registers one step ahead (the codes become BF16
+// on the way) into one of two. Per wave and step:
 //   QK   for each block and set, four v_mfma_f32_16x16x32_bf16 on K read from LDS (lane
 //        (g, n): key n, dims 32g + 8j .. +8), reused by both sets;
 //   P    8 scores per lane (keys 4g..4g+3 of each block) of row n;
@@ -294,27 +294,49 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_mfma(PrefillArgs
 //        weights as the numerator. FP8 pools weight P by the V block's 2^shift, so their
 //        sums stay per-lane VALU adds of the unscaled weights.
 // Causal masking runs only in steps that reach past the wave's first row's limit (the later
-// rows of a wave only see more keys). K rows are padded to 272 bytes, so the 16 lanes reading
-// one column of 16 rows with 16-byte reads hit distinct banks; V rows to 288 bytes, so the 16
-// lanes of a group fetching 8 bytes from 4 rows at 4 offsets cover 32 distinct banks.
+// rows of a wave only see more keys). The tiles' LDS layout (k_slot, v_slot below) has no row
+// padding, which direct-to-LDS copies cannot write, and is swizzled instead so that the K reads
+// hit distinct banks and the V reads stay within one region.
 // Registers are held to 256 per lane (amdgpu_waves_per_eu(2)), so two workgroups share a CU
 // and one computes while the other waits at its step barrier. Measured on MI355X at a
 // 2,048-token chunk ending a 32,768-token context: 2.97 ms per layer at one wave per SIMD and
 // 1.61 ms at two; 1.39 ms with conflict-free LDS stores, one FMA per weight's exponent, 32-bit
 // causal compares and permlane-swapped row maxima, with V regrouped by 32 v_perm per step;
 // 1.18 ms with the transposing V reads, per-set stretches, masks only where needed and the
-// sums on the matrix cores.
+// sums on the matrix cores; 1.13 ms with the lane-local rescale check; 1.10 ms with the
+// direct-to-LDS copies two steps ahead into the swizzled layout.
 // O leaves through LDS: its rows are spread over lanes by dim (16e + n), so each wave writes
 // its 32 rows there and reads them back as 16-byte pieces of whole rows.
 constexpr uint32_t kLdsWaves = 4;
-constexpr uint32_t kLdsRows = 32;                       // rows per wave
-constexpr uint32_t kLdsRowBytes = kDim * 2 + 16;        // 272: K rows
-constexpr uint32_t kLdsVRowBytes = kDim * 2 + 32;       // 288: V rows
-constexpr uint32_t kLdsTile = kSlots * kLdsRowBytes;    // one block's K
-constexpr uint32_t kLdsVTile = kSlots * kLdsVRowBytes;  // one block's V
-constexpr uint32_t kLdsStep = 2 * kLdsTile + 2 * kLdsVTile;  // K0, K1, V0, V1
-constexpr uint32_t kLdsBuffers = 2;  // step i is read from one while step i + 1 is stored
-static_assert(kLdsWaves * kLdsRows * kLdsRowBytes <= kLdsBuffers * kLdsStep, "the output staging must fit the step buffers");
+constexpr uint32_t kLdsRows = 32;                        // rows per wave
+constexpr uint32_t kLdsRowBytes = kDim * 2 + 16;         // 272: rows of the output staging
+// A step's tiles (K0, K1, V0, V1: 16 keys x 256 bytes each) are laid out without row padding,
+// each as four 1 KiB regions 16 bytes apart; a region is what one 16-byte-per-lane copy of a
+// wave fills. K region x holds keys 4x .. 4x+3, their 16-byte chunks XOR-swizzled by
+// 4 * (key % 4), so the 16 lanes reading one chunk of 16 keys hit 16 different bank quads.
+// V region x holds chunks 4x .. 4x+3 (dims 32x .. 32x+31) of all 16 keys, 64 bytes a key, so
+// the transposing reads (keys 4g .. 4g+3, 8 bytes each, of one dim group) stay in one region.
+constexpr uint32_t kRegionStride = 1024 + 16;
+constexpr uint32_t kLdsTile = 4 * kRegionStride;         // one block's K or V
+constexpr uint32_t kLdsStep = 4 * kLdsTile;              // K0, K1, V0, V1
+constexpr uint32_t kLdsAllocated = 3;  // step buffers allocated (FP8 rotates through two)
+static_assert(kLdsWaves * kLdsRows * kLdsRowBytes <= kLdsAllocated * kLdsStep, "the output staging must fit the step buffers");
+
+// Byte offset of key `key`'s 16-byte chunk `chunk` (dims 8 chunk .. +8) inside a K or V tile.
+__device__ __forceinline__ uint32_t k_slot(uint32_t key, uint32_t chunk) {
+    return (key / 4) * kRegionStride + (key % 4) * 256 + 16 * (chunk ^ (4 * (key % 4)));
+}
+__device__ __forceinline__ uint32_t v_slot(uint32_t key, uint32_t chunk) {
+    return (chunk / 4) * kRegionStride + key * 64 + 16 * (chunk % 4);
+}
+
+// BF16 pools copy each step straight into LDS two steps ahead (three buffers); FP8 pools
+// convert their codes on the way, through registers, one step ahead (two buffers).
+template <int KV>
+constexpr uint32_t lds_buffers() {
+    return KV == LK_BF16 ? 3 : 2;
+}
+constexpr uint32_t kCopiesPerStep = 4;  // 16-byte-per-lane copies per wave and step (BF16)
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
@@ -333,7 +355,9 @@ struct PrefillStaged {
 
 template <int KV>
 __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_mfma_lds(PrefillArgs a) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBuffers][kLdsStep];
+    constexpr uint32_t kLdsBuffers = lds_buffers<KV>();
+    static_assert(kLdsBuffers <= kLdsAllocated, "more step buffers than allocated");
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsAllocated][kLdsStep];
     __shared__ int32_t lds_shift[kLdsBuffers][4];  // FP8: per buffer, the shift of K0, K1, V0, V1
     const uint32_t lane = threadIdx.x % kWave;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -395,47 +419,68 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
     const uint64_t group = part < 2 ? head_tile : uint64_t(a.layers) * a.kv_heads + head_tile;
     const uint64_t part_offset = group * tile_bytes + uint64_t(piece) * 8 * kElem;
     const uint64_t block_elems = uint64_t(2) * a.layers * a.kv_heads * kSlots * kDim;
-    // Value 512x + 8t sits in slot 4x + t / 16, dims 8 (t % 16) .. +8.
-    const uint32_t row_bytes = part < 2 ? kLdsRowBytes : kLdsVRowBytes;
-    const uint32_t lds_offset =
-        (part < 2 ? part * kLdsTile : 2 * kLdsTile + (part - 2) * kLdsVTile) + (piece / 16) * row_bytes + (piece % 16) * 16;
+    // Value 512x + 8t of a tile is key 4x + t / 16, chunk t % 16; where it goes in LDS:
+    const uint32_t tile_lds = part * kLdsTile;
+    auto slot_of = [&](uint32_t x) __attribute__((always_inline)) {
+        const uint32_t key = 4 * x + piece / 16, chunk = piece % 16;
+        return tile_lds + (part < 2 ? k_slot(key, chunk) : v_slot(key, chunk));
+    };
     auto load_step = [&](uint32_t step, PrefillStaged& r) __attribute__((always_inline)) {
         const uint32_t block_index = min(2 * step + (part & 1), last_block);
         const int32_t block = a.block_ids[block_index];
         const uint8_t* base = a.pool + uint64_t(uint32_t(block)) * a.block_bytes + part_offset;
-        if constexpr (KV == LK_BF16) {
-            r.w0 = *reinterpret_cast<const u32x4*>(base);
-            r.w1 = *reinterpret_cast<const u32x4*>(base + 1024);
-            r.w2 = *reinterpret_cast<const u32x4*>(base + 2048);
-            r.w3 = *reinterpret_cast<const u32x4*>(base + 3072);
-        } else {
-            const u32x2 c0 = *reinterpret_cast<const u32x2*>(base), c1 = *reinterpret_cast<const u32x2*>(base + 512);
-            const u32x2 c2 = *reinterpret_cast<const u32x2*>(base + 1024), c3 = *reinterpret_cast<const u32x2*>(base + 1536);
-            r.w0 = u32x4{c0[0], c0[1], c1[0], c1[1]};
-            r.w1 = u32x4{c2[0], c2[1], c3[0], c3[1]};
-            r.shift = reinterpret_cast<const int16_t*>(a.pool + uint64_t(uint32_t(block)) * a.block_bytes + block_elems)[group];
-        }
+        const u32x2 c0 = *reinterpret_cast<const u32x2*>(base), c1 = *reinterpret_cast<const u32x2*>(base + 512);
+        const u32x2 c2 = *reinterpret_cast<const u32x2*>(base + 1024), c3 = *reinterpret_cast<const u32x2*>(base + 1536);
+        r.w0 = u32x4{c0[0], c0[1], c1[0], c1[1]};
+        r.w1 = u32x4{c2[0], c2[1], c3[0], c3[1]};
+        r.shift = reinterpret_cast<const int16_t*>(a.pool + uint64_t(uint32_t(block)) * a.block_bytes + block_elems)[group];
     };
     auto store_step = [&](uint32_t buffer, const PrefillStaged& r) __attribute__((always_inline)) {
-        uint8_t* dst = lds[buffer] + lds_offset;
-        if constexpr (KV == LK_BF16) {
-            *reinterpret_cast<u32x4*>(dst) = r.w0;
-            *reinterpret_cast<u32x4*>(dst + 4 * row_bytes) = r.w1;
-            *reinterpret_cast<u32x4*>(dst + 8 * row_bytes) = r.w2;
-            *reinterpret_cast<u32x4*>(dst + 12 * row_bytes) = r.w3;
-        } else {
-            // Chunk x's 8 codes are words (2x, 2x + 1) of w0, w1.
-            const bool exact = !shift_is_exact_in_fp32(r.shift);
-            auto convert = [&](uint32_t lo, uint32_t hi) __attribute__((always_inline)) {
-                return u32x4{fp8_pair(lo, false, exact, r.shift), fp8_pair(lo, true, exact, r.shift), fp8_pair(hi, false, exact, r.shift),
-                             fp8_pair(hi, true, exact, r.shift)};
-            };
-            *reinterpret_cast<u32x4*>(dst) = convert(r.w0[0], r.w0[1]);
-            *reinterpret_cast<u32x4*>(dst + 4 * row_bytes) = convert(r.w0[2], r.w0[3]);
-            *reinterpret_cast<u32x4*>(dst + 8 * row_bytes) = convert(r.w1[0], r.w1[1]);
-            *reinterpret_cast<u32x4*>(dst + 12 * row_bytes) = convert(r.w1[2], r.w1[3]);
-            if (piece == 0) lds_shift[buffer][part] = r.shift;
-        }
+        uint8_t* dst = lds[buffer];
+        // Chunk x's 8 codes are words (2x, 2x + 1) of w0, w1.
+        const bool exact = !shift_is_exact_in_fp32(r.shift);
+        auto convert = [&](uint32_t lo, uint32_t hi) __attribute__((always_inline)) {
+            return u32x4{fp8_pair(lo, false, exact, r.shift), fp8_pair(lo, true, exact, r.shift), fp8_pair(hi, false, exact, r.shift),
+                         fp8_pair(hi, true, exact, r.shift)};
+        };
+        *reinterpret_cast<u32x4*>(dst + slot_of(0)) = convert(r.w0[0], r.w0[1]);
+        *reinterpret_cast<u32x4*>(dst + slot_of(1)) = convert(r.w0[2], r.w0[3]);
+        *reinterpret_cast<u32x4*>(dst + slot_of(2)) = convert(r.w1[0], r.w1[1]);
+        *reinterpret_cast<u32x4*>(dst + slot_of(3)) = convert(r.w1[2], r.w1[3]);
+        if (piece == 0) lds_shift[buffer][part] = r.shift;
+    };
+
+    // BF16 pools: wave w copies tile w of a step straight into its LDS buffer, one 1 KiB region
+    // per instruction (lane t writes bytes 16t .. 16t+15 of the region), so lane t fetches the
+    // chunk the layout puts there: for K key 4x + t/16, chunk (t % 16) ^ 4(t/16); for V key
+    // t/4, chunk 4x + t % 4. The copies are issued as inline assembly, which the compiler's wait
+    // counting does not see (it would otherwise wait for them before any LDS read it cannot
+    // prove disjoint); they are waited for only at the barrier before their step is read (see
+    // step_barrier), which relies on exactly kCopiesPerStep of them per wave and step and no
+    // other vector-memory loads in the loop (block ids are scalar loads).
+    const auto* scalar_ids = (const __attribute__((address_space(4))) int32_t*)a.block_ids;
+    const uint32_t wave_part = __builtin_amdgcn_readfirstlane(part);
+    const uint32_t copy_src = wave_part < 2 ? (piece / 16) * 256 + 16 * ((piece % 16) ^ (4 * (piece / 16))) : (piece / 4) * 256 + 16 * (piece % 4);
+    const uint32_t copy_step = wave_part < 2 ? 1024 : 64;  // source bytes between regions
+    const uint64_t copy_tile = group * tile_bytes;
+    auto copy_step_tiles = [&](uint32_t step) __attribute__((always_inline)) {
+        const uint32_t block_index = min(2 * step + (wave_part & 1), last_block);
+        const uint32_t block = uint32_t(scalar_ids[block_index]);
+        const uint8_t* src = a.pool + uint64_t(block) * a.block_bytes + copy_tile + copy_src;
+        const uint32_t dst = uint32_t(uintptr_t((__attribute__((address_space(3))) uint8_t*)(lds[step % kLdsBuffers] + tile_lds)));
+#pragma unroll
+        for (uint32_t x = 0; x < kCopiesPerStep; ++x)
+            asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src + copy_step * x),
+                         "s"(__builtin_amdgcn_readfirstlane(dst + kRegionStride * x))
+                         : "memory", "m0");
+    };
+    // The end of a BF16 step: this wave's copies of the step after next may stay in flight; the
+    // older ones, which fill the next step's buffer, must have landed, and every LDS read of
+    // this step must be done before any wave refills its buffer.
+    auto step_barrier = [&](bool copies_in_flight) __attribute__((always_inline)) {
+        static_assert(kCopiesPerStep == 4, "the wait below counts the copies");
+        if (copies_in_flight) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     };
 
     // Running maximum per row (lane (g, n): row n of each set); output and, for BF16 pools,
@@ -450,8 +495,11 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
     }
     const bf16x8 ones = as_bf16x8(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
 
-    // Transposing V reads: lane 4t + q of group g fetches key 4g + t, dims 16e + 4q .. +3.
-    const uint32_t v_read = 2 * kLdsTile + (4 * g + n / 4) * kLdsVRowBytes + (n % 4) * 8;
+    // Transposing V reads: lane 4t + q of group g fetches key 4g + t, dims 16e + 4q .. +3,
+    // i.e. bytes 8q .. 8q+7 of chunks 2e, 2e + 1 (region e / 2, offset 32 (e % 2)).
+    const uint32_t v_read = 2 * kLdsTile + (4 * g + n / 4) * 64 + (n % 4) * 8;
+    // K reads: lane (g, n) reads key n's chunks 4g .. 4g+3, stored at 4(g ^ (n % 4)) + j.
+    const uint32_t k_read = (n / 4) * kRegionStride + (n % 4) * 256 + 64 * (g ^ (n % 4));
 
     // Per step: the scale of each block's scores (log2 units) and of its weights.
     struct Factors {
@@ -477,7 +525,7 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
         const uint8_t* buf = lds[step % kLdsBuffers];
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
-            const uint8_t* k_row = buf + b * kLdsTile + n * kLdsRowBytes + 64 * g;
+            const uint8_t* k_row = buf + b * kLdsTile + k_read;
 #pragma unroll
             for (int j = 0; j < 4; ++j) kk[b][j] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(k_row + 16 * j));
         }
@@ -500,9 +548,9 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
         const auto* buf = (const __attribute__((address_space(3))) uint8_t*)(lds[step % kLdsBuffers]);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const auto* at = buf + v_read + 32 * e;
+            const auto* at = buf + v_read + (e / 2) * kRegionStride + 32 * (e % 2);
             const i16x4 v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(at));
-            const i16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(at + kLdsVTile));
+            const i16x4 v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(at + kLdsTile));
             const u32x2 w0 = __builtin_bit_cast(u32x2, v0), w1 = __builtin_bit_cast(u32x2, v1);
             vb[e] = u32x4{w0[0], w0[1], w1[0], w1[1]};
         }
@@ -601,6 +649,9 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
     // barriers measured 4% slower: the two waves on each SIMD already overlap each other.
     auto run_step = [&](uint32_t step, auto masked_tag) __attribute__((always_inline)) {
         constexpr bool kMasked = decltype(masked_tag)::value;
+        if constexpr (KV == LK_BF16) {
+            if (step + 2 < steps) copy_step_tiles(step + 2);
+        }
         const Factors f = factors(step);
         bf16x8 kk[2][4];
         read_k(step, kk);
@@ -637,18 +688,31 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
         accumulate(0, p0, vb);
         const bf16x8 p1 = weights(1, s[1], f);
         accumulate(1, p1, vb);
-        if (step + 1 < steps) {
-            store_step((step + 1) % kLdsBuffers, staged);
-            if (step + 2 < steps) load_step(step + 2, staged);
+        if constexpr (KV == LK_BF16) {
+            step_barrier(step + 2 < steps);
+        } else {
+            if (step + 1 < steps) {
+                store_step((step + 1) % kLdsBuffers, staged);
+                if (step + 2 < steps) load_step(step + 2, staged);
+            }
+            __syncthreads();
         }
-        __syncthreads();
     };
 
     if (first_step < steps) {
-        load_step(first_step, staged);
-        store_step(first_step % kLdsBuffers, staged);
-        if (first_step + 1 < steps) load_step(first_step + 1, staged);
-        __syncthreads();
+        if constexpr (KV == LK_BF16) {
+            // Q's loads must be complete (and known to be) before the first copy: a wait for
+            // them inside the loop would count the copies issued after them.
+            __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+            copy_step_tiles(first_step);
+            if (first_step + 1 < steps) copy_step_tiles(first_step + 1);
+            step_barrier(false);
+        } else {
+            load_step(first_step, staged);
+            store_step(first_step % kLdsBuffers, staged);
+            if (first_step + 1 < steps) load_step(first_step + 1, staged);
+            __syncthreads();
+        }
         // Steps whose 32 keys all lie at or below the wave's first row's limit need no mask.
         const uint32_t unmasked = first_limit < 0 ? 0u : min(steps, uint32_t((first_limit + 1) / (2 * kSlots)));
         uint32_t step = first_step;
