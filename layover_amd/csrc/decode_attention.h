@@ -116,8 +116,8 @@ __device__ __forceinline__ uint32_t blocks_of(int32_t length, uint32_t slots) { 
 //
 // A wave takes one (block, KV head) unit at a time; lane l is (g, n) = (l / 16, l % 16).
 //   QK:  S^T[slot][head] = sum_d K[slot][d] q[head][d] with v_mfma_f32_16x16x32_bf16, four
-//        steps over the 128 dims. A = K: lane (g, n) holds slot n, dims 32g + 8j .. +8 for
-//        step j, so its 4 A operands are the 64 contiguous bytes at dims 32g (BF16; FP8 codes
+//        steps over the 128 dims. A = K: lane (g, n) holds slot n and, for step j, 8 dims
+//        chosen per format so the loads stay contiguous (MfmaTile) (BF16; FP8 codes
 //        are converted to BF16 exactly in registers). B = q^T, the same dims of query head n
 //        (zero for n >= G): up to 16 query heads per KV head cost nothing extra.
 //        The result lands as lane (g, n) = head n, slots 4g .. 4g+3.
@@ -146,17 +146,23 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 template <int KV>
 struct MfmaTile;
+// Lane group g of K holds, for QK step j, the dims kGroupDims * g + kStepDims * j .. +8 of
+// slot n (q's B operand uses the same dims). BF16: 8g + 32j, so each of the four K load
+// instructions reads 64 contiguous bytes of every slot row (whole 64-byte halves of its
+// 128-byte lines). FP8: 32g + 8j, one 32-byte run of codes per lane.
 template <>
 struct MfmaTile<LK_BF16> {
-    uint32_t k[16];     // slot n, dims 32g .. 32g+31 (BF16 pairs)
+    uint32_t k[16];     // slot n, dims 8g + 32j .. +8 for j = 0..3 (BF16 pairs)
     uint32_t v[4][4];   // slot 4g + r, dims 8n .. 8n+7 (BF16 pairs)
     static constexpr int32_t k_shift = 0, v_shift = 0;
+    static constexpr uint32_t kGroupDims = 8, kStepDims = 32;
 };
 template <>
 struct MfmaTile<LK_FP8_RECORD> {
     uint32_t k[8];      // slot n, dims 32g .. 32g+31 (E4M3 codes)
     uint32_t v[4][2];   // slot 4g + r, dims 8n .. 8n+7 (E4M3 codes)
     int32_t k_shift, v_shift;
+    static constexpr uint32_t kGroupDims = 32, kStepDims = 8;
 };
 
 // A shift for which every E4M3 code times 2**shift is zero, NaN or a BF16 normal below
@@ -185,12 +191,16 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
 
-// Register buffers per wave (see the main loop of decode_split_mfma).
+// Register buffers per wave (see the main loop of decode_split_mfma). Two for both formats,
+// measured on MI355X per layer (Qwen3-4B): BF16 batch 32 mixed contexts on distinct blocks
+// 389 -> 377-383 us with three, batch 1 @ 32,768 34.1 -> 32.4 us; FP8 batch 64 @ 4,096
+// 86.1 -> 82.7 us and batch 1 23.5 -> 22.3 us against four. More buffers in flight per wave
+// do not buy bandwidth here, and cost registers and issue slots.
 #ifndef LK_DECODE_RING_BF16
-#define LK_DECODE_RING_BF16 3
+#define LK_DECODE_RING_BF16 2
 #endif
 #ifndef LK_DECODE_RING_FP8
-#define LK_DECODE_RING_FP8 4
+#define LK_DECODE_RING_FP8 2
 #endif
 
 // Workgroup -> (sequence, split, KV head). Order 1 (the default): KV head fastest, so the
@@ -233,8 +243,9 @@ __global__ __launch_bounds__(kWave* kDecodeWaves) void decode_split_mfma(DecodeA
     const int32_t listed_block = lane < listed ? row_ids[wave + lane * kDecodeWaves] : 0;
     const int32_t length = a.lengths[uint64_t(seq) * a.lengths_stride];
 
-    // B operands of QK: query head n (zero past the group), dims 32g + 8j .. +8 for step j.
-    // An FP32 q is split into BF16 hi + lo parts, one MFMA each.
+    // B operands of QK: query head n (zero past the group), the dims kDimsOf(g, j) .. +8 that
+    // lane group g of K holds for step j. An FP32 q is split into BF16 hi + lo parts, one MFMA
+    // each.
     constexpr int kQParts = QF == LK_BF16 ? 1 : 2;
     uint32_t qt[kQParts][16];
 #pragma unroll
@@ -242,18 +253,19 @@ __global__ __launch_bounds__(kWave* kDecodeWaves) void decode_split_mfma(DecodeA
 #pragma unroll
         for (int i = 0; i < 16; ++i) qt[part][i] = 0;
     if (n < groups) {
-        const uint64_t row_at = (uint64_t(seq) * a.query_heads + kv_head * groups + n) * kDim + 32 * g;
+        const uint64_t row_at = (uint64_t(seq) * a.query_heads + kv_head * groups + n) * kDim + MfmaTile<KV>::kGroupDims * g;
+        constexpr uint32_t kStepDims = MfmaTile<KV>::kStepDims;
         if constexpr (QF == LK_BF16) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const u32x4 w = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(a.q) + row_at)[j];
+                const u32x4 w = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(a.q) + row_at + j * kStepDims);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) qt[0][4 * j + i] = w[i];
             }
         } else {
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const u32x4 w = reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(a.q) + row_at)[j];
+                const u32x4 w = *reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(a.q) + row_at + (j / 2) * kStepDims + 4 * (j % 2));
 #pragma unroll
                 for (int i = 0; i < 2; ++i) {
                     const float x0 = __uint_as_float(w[2 * i]), x1 = __uint_as_float(w[2 * i + 1]);
@@ -273,7 +285,7 @@ __global__ __launch_bounds__(kWave* kDecodeWaves) void decode_split_mfma(DecodeA
     constexpr uint32_t kElem = KV == LK_FP8_RECORD ? 1 : 2;
     const uint64_t tile_bytes = uint64_t(kSlots) * kDim * kElem;
     const uint64_t head_tile = uint64_t(a.layer) * a.kv_heads + kv_head;  // group index of K
-    const uint64_t k_offset = head_tile * tile_bytes + (uint64_t(n) * kDim + 32 * g) * kElem;
+    const uint64_t k_offset = head_tile * tile_bytes + (uint64_t(n) * kDim + MfmaTile<KV>::kGroupDims * g) * kElem;
     const uint64_t v_offset = (uint64_t(a.layers) * a.kv_heads + head_tile) * tile_bytes + (uint64_t(4 * g) * kDim + 8 * n) * kElem;
     const uint64_t block_elems = uint64_t(2) * a.layers * a.kv_heads * kSlots * kDim;  // FP8: shifts follow the data
 
@@ -297,7 +309,7 @@ __global__ __launch_bounds__(kWave* kDecodeWaves) void decode_split_mfma(DecodeA
         if constexpr (KV == LK_BF16) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const u32x4 w = reinterpret_cast<const u32x4*>(base + k_offset)[j];
+                const u32x4 w = *reinterpret_cast<const u32x4*>(base + k_offset + j * MfmaTile<KV>::kStepDims * kElem);
 #pragma unroll
                 for (int x = 0; x < 4; ++x) tile.k[4 * j + x] = w[x];
             }
