@@ -19,7 +19,7 @@ Also measured in the same run (extra keys of the JSON line):
               32,768-token context, beside gather + torch flash attention on the same GPU
   overlap     configs[4]: decode steps while 2,048 blocks swap out and back in
   decode_distinct  configs[2] on a ~78 GB pool whose rows share no block
-  hbm_probe   lk_stream_probe read and copy rates: the measured HBM ceiling
+  hbm_probe   lk_stream_probe read and copy rates and lk_stream_probe_mix at the FP8 kernels' read/write mixes: the measured HBM ceilings
   cpu_baseline  the oracle's C restatement of the FP8 swap arithmetic on a bounded sample,
               single-threaded on the host cores
   cpu_reference_config1  configs[0] on the reference's own host library (oracle/_ref)
@@ -126,9 +126,11 @@ def measure_link(device, nbytes: int = 512 << 20, repeats: int = 5) -> dict:
 
 
 def measure_hbm(device, nbytes: int = 8 << 30, repeats: int = 5) -> dict:
-    """HBM ceilings measured on this GPU with the library's streaming probe (16-byte loads,
-    grid-stride, several loads in flight per lane): read-only over 8 GiB, and a copy of 4 GiB
-    (8 GiB of traffic). Reported beside the 8 TB/s specification."""
+    """HBM ceilings measured on this GPU with the library's streaming probes (each wave moves
+    one contiguous 4 KiB chunk once, non-temporal): read-only over 8 GiB, a copy of 4 GiB
+    (8 GiB of traffic), and the two traffic mixes of the FP8 record kernels: 8 GiB read and
+    4 GiB written (quantize's 2:1), 4 GiB read and 8 GiB written (dequantize's 1:2). Reported
+    beside the 8 TB/s specification; rates count bytes read plus bytes written."""
     import torch
 
     from layover_amd.kernels import _lib
@@ -136,13 +138,16 @@ def measure_hbm(device, nbytes: int = 8 << 30, repeats: int = 5) -> dict:
     lib = _lib.load()
     src = torch.empty(nbytes, dtype=torch.uint8, device=device)
     src.fill_(1)
-    dst = torch.empty(nbytes // 2, dtype=torch.uint8, device=device)
+    dst = torch.empty(nbytes, dtype=torch.uint8, device=device)
     sink = torch.zeros(1, dtype=torch.int32, device=device)
     stream = _lib.current_stream(device)
+    half = nbytes // 2
     out = {}
     for name, run, moved in (
         ("read_gbs", lambda: lib.lk_stream_probe(src.data_ptr(), None, nbytes, sink.data_ptr(), stream), nbytes),
-        ("copy_gbs", lambda: lib.lk_stream_probe(src.data_ptr(), dst.data_ptr(), nbytes // 2, sink.data_ptr(), stream), nbytes),
+        ("copy_gbs", lambda: lib.lk_stream_probe(src.data_ptr(), dst.data_ptr(), half, sink.data_ptr(), stream), nbytes),
+        ("quantize_mix_gbs", lambda: lib.lk_stream_probe_mix(src.data_ptr(), nbytes, dst.data_ptr(), half, stream), nbytes + half),
+        ("dequantize_mix_gbs", lambda: lib.lk_stream_probe_mix(src.data_ptr(), half, dst.data_ptr(), nbytes, stream), nbytes + half),
     ):
         _lib.check(run())
         torch.cuda.synchronize()
@@ -772,7 +777,17 @@ def main() -> None:
     # Last, so its 12 GiB of buffers come and go after everything timed above.
     log("HBM probe")
     result["hbm_probe"] = {k: round(v, 1) for k, v in measure_hbm(device).items()}
-    result["hbm_probe"]["kind"] = "lk_stream_probe: read 8 GiB; copy 4 GiB (8 GiB of traffic)"
+    result["hbm_probe"]["kind"] = (
+        "lk_stream_probe: read 8 GiB; copy 4 GiB (8 GiB of traffic); lk_stream_probe_mix: 8 GiB read + 4 GiB written "
+        "(quantize's 2:1), 4 GiB read + 8 GiB written (dequantize's 1:2)"
+    )
+    if "roofline" in result:
+        # The quantize kernel against the measured ceiling for its own read/write mix.
+        result["hbm_probe"]["quantize_frac_of_mix"] = round(result["roofline"]["achieved"] / result["hbm_probe"]["quantize_mix_gbs"], 3)
+    if "dequantize_kernel" in result:
+        result["hbm_probe"]["dequantize_frac_of_mix"] = round(
+            result["dequantize_kernel"]["achieved_gbs"] / result["hbm_probe"]["dequantize_mix_gbs"], 3
+        )
 
     if not args.skip_cpu:
         log(f"cpu baseline: oracle FP8 quantize+dequantize on {args.cpu_blocks} blocks")

@@ -168,6 +168,13 @@ int lk_fp8_append(void* records, const int32_t* write_block, const int32_t* writ
  * the HBM ceiling bench.py reports beside the 8 TB/s specification. */
 int lk_stream_probe(const void* src, void* dst, uint64_t bytes, uint32_t* sink, void* stream);
 
+/* Measurement support, no reference counterpart: the traffic mix of the FP8 record kernels.
+ * Reads `src_bytes` from `src` and writes `dst_bytes` to `dst`, in the ratio 2:1 (as
+ * lk_fp8_quantize: src_bytes a multiple of 4096) or 1:2 (as lk_fp8_dequantize: a multiple of
+ * 2048), each wave moving one contiguous chunk of each. The measured ceiling for those kernels'
+ * mix of reads and writes; LK_ERR_INVALID for any other ratio. */
+int lk_stream_probe_mix(const void* src, uint64_t src_bytes, void* dst, uint64_t dst_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

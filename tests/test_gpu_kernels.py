@@ -401,3 +401,52 @@ def test_decode_block_offsets_past_32_bits(hip_decode):
     assert_close_to_oracle(out, expected, "64-bit offsets")
     del pool
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("nbytes", [16, 4096, 16 * 1024, 5 * 4096 + 48, 3 << 20])
+def test_stream_probe_reads_without_writing_and_copies_exactly(nbytes):
+    """lk_stream_probe: a read leaves the sink alone; a copy (partial last chunk included)
+    reproduces the source and writes nothing past `bytes`."""
+    from layover_amd.kernels import _lib
+
+    lib = _lib.load()
+    stream = _lib.current_stream(torch.device("cuda"))
+    gen = torch.Generator(device="cuda").manual_seed(nbytes)
+    src = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device="cuda", generator=gen)
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    _lib.check(lib.lk_stream_probe(src.data_ptr(), None, nbytes, sink.data_ptr(), stream))
+    dst = torch.full((nbytes + 4096,), 0xA5, dtype=torch.uint8, device="cuda")
+    _lib.check(lib.lk_stream_probe(src.data_ptr(), dst.data_ptr(), nbytes, sink.data_ptr(), stream))
+    torch.cuda.synchronize()
+    assert int(sink.item()) == 0
+    assert torch.equal(dst[:nbytes], src)
+    assert bool((dst[nbytes:] == 0xA5).all())
+
+
+@pytest.mark.parametrize("ratio", ["2:1", "1:2"])
+def test_stream_probe_mix_moves_the_stated_bytes(ratio):
+    """lk_stream_probe_mix: 2:1 writes, per 16-byte lane word k of a chunk's output, the XOR
+    of input words 2k and 2k + 1 of that lane; 1:2 writes input word k // 2. Nothing is written
+    past dst_bytes, and other ratios are refused."""
+    from layover_amd.kernels import _lib
+
+    lib = _lib.load()
+    stream = _lib.current_stream(torch.device("cuda"))
+    chunks = 37
+    read_chunk = 4096 if ratio == "2:1" else 2048
+    src_bytes = chunks * read_chunk
+    dst_bytes = src_bytes // 2 if ratio == "2:1" else src_bytes * 2
+    src = torch.randint(0, 2**31, (src_bytes // 4,), dtype=torch.int32, device="cuda")
+    dst = torch.full((dst_bytes // 4 + 1024,), -7, dtype=torch.int32, device="cuda")
+    _lib.check(lib.lk_stream_probe_mix(src.data_ptr(), src_bytes, dst.data_ptr(), dst_bytes, stream))
+    torch.cuda.synchronize()
+    # [chunk, word k, lane, 4 dwords]
+    words_in = src.view(chunks, read_chunk // 1024, 64, 4).cpu()
+    if ratio == "2:1":
+        expect = words_in[:, 0::2] ^ words_in[:, 1::2]
+    else:
+        expect = words_in.repeat_interleave(2, dim=1)
+    assert torch.equal(dst[: dst_bytes // 4].cpu().view_as(expect), expect)
+    assert bool((dst[dst_bytes // 4 :] == -7).all())
+    with pytest.raises(_lib.KernelError):
+        _lib.check(lib.lk_stream_probe_mix(src.data_ptr(), src_bytes, dst.data_ptr(), src_bytes, stream))
