@@ -171,13 +171,16 @@ __device__ __forceinline__ void dequantize_load(const uint8_t* __restrict__ stag
     in.group = group;
 }
 
-__device__ __forceinline__ void dequantize_finish(uint16_t* __restrict__ pool, uint32_t groups_per_block, uint32_t lane, const DequantizeLoad& in) {
-    const uint32_t g = uint32_t(in.group % groups_per_block);
-    const uint64_t block_elems = uint64_t(kFastGroup) * groups_per_block;
-    const int32_t shift = in.shift;
-    u32x4* target = reinterpret_cast<u32x4*>(pool + uint64_t(uint32_t(in.block)) * block_elems + uint64_t(g) * kFastGroup);
-    const u32x2* bytes = in.bytes;
+// One group's codes (lane's 4 x 8 bytes) at `shift` to BF16, stored as 4 x 16 bytes per lane
+// at `target` (2,048 values); non-temporal stores unless the values are read again soon.
+template <bool kNontemporal = true>
+__device__ __forceinline__ void store_bf16(u32x4* target, u32x4 value) {
+    if constexpr (kNontemporal) __builtin_nontemporal_store(value, target);
+    else *target = value;
+}
 
+template <bool kNontemporal = true>
+__device__ __forceinline__ void decode_group_to(u32x4* __restrict__ target, int32_t shift, const u32x2* bytes, uint32_t lane) {
     // A byte 0x7F or 0xFF (NaN) becomes 0x80 after masking off its sign and adding one.
     uint32_t flags = 0;
 #pragma unroll
@@ -197,7 +200,7 @@ __device__ __forceinline__ void dequantize_finish(uint16_t* __restrict__ pool, u
                 out[2 * w] = __builtin_amdgcn_perm(__float_as_uint(lo.y * scale), __float_as_uint(lo.x * scale), 0x07060302u);
                 out[2 * w + 1] = __builtin_amdgcn_perm(__float_as_uint(hi.y * scale), __float_as_uint(hi.x * scale), 0x07060302u);
             }
-            __builtin_nontemporal_store(out, target + j * kWave + lane);
+            store_bf16<kNontemporal>(target + j * kWave + lane, out);
         }
     } else {
 #pragma unroll
@@ -208,9 +211,16 @@ __device__ __forceinline__ void dequantize_finish(uint16_t* __restrict__ pool, u
                 const uint32_t word = bytes[j][w / 2] >> (16 * (w % 2));
                 out[w] = decode_e4m3(word & 0xFFu, shift) | (decode_e4m3((word >> 8) & 0xFFu, shift) << 16);
             }
-            __builtin_nontemporal_store(out, target + j * kWave + lane);
+            store_bf16<kNontemporal>(target + j * kWave + lane, out);
         }
     }
+}
+
+__device__ __forceinline__ void dequantize_finish(uint16_t* __restrict__ pool, uint32_t groups_per_block, uint32_t lane, const DequantizeLoad& in) {
+    const uint32_t g = uint32_t(in.group % groups_per_block);
+    const uint64_t block_elems = uint64_t(kFastGroup) * groups_per_block;
+    decode_group_to(reinterpret_cast<u32x4*>(pool + uint64_t(uint32_t(in.block)) * block_elems + uint64_t(g) * kFastGroup), in.shift, in.bytes,
+                    lane);
 }
 
 __global__ __launch_bounds__(kWave* kCodecWaves) void dequantize_groups_2048(const uint8_t* __restrict__ stage,
@@ -236,6 +246,40 @@ __global__ __launch_bounds__(kWave* kCodecWaves) void dequantize_groups_2048(con
         dequantize_finish(pool, groups_per_block, lane, odd);
         ++group;
     }
+}
+
+// One layer of a sequence's history, FP8 records to BF16 for the paged prefill: wave w takes
+// group (block b, kind, KV head) = (w / (2 kv_heads), w / kv_heads % 2, w % kv_heads) of
+// block ids[b], and writes it to stage[b][kind][head] (16 x 128 BF16, a one-layer pool block);
+// the first wave of each block also writes index[b] = b. Same decode, bit for bit, as
+// dequantize_groups_2048.
+__global__ __launch_bounds__(kWave* kCodecWaves) void stage_history_2048(const uint8_t* __restrict__ records,
+                                                                       const int32_t* __restrict__ ids, uint64_t record_bytes,
+                                                                       uint32_t groups_per_block, uint32_t layer, uint32_t layers,
+                                                                       uint32_t kv_heads, uint32_t blocks, uint16_t* __restrict__ stage,
+                                                                       int32_t* __restrict__ index) {
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint64_t unit = uint64_t(blockIdx.x) * kCodecWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    if (unit >= uint64_t(blocks) * 2 * kv_heads) return;
+    const uint32_t b = uint32_t(unit / (2 * kv_heads));
+    const uint32_t kind = uint32_t(unit / kv_heads % 2), head = uint32_t(unit % kv_heads);
+    const uint8_t* record = records + uint64_t(uint32_t(ids[b])) * record_bytes;
+    const uint64_t group = (uint64_t(kind) * layers + layer) * kv_heads + head;
+    const u32x2* codes = reinterpret_cast<const u32x2*>(record + group * kFastGroup);
+    u32x2 bytes[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bytes[j] = __builtin_nontemporal_load(codes + j * kWave + lane);
+    const int32_t shift = reinterpret_cast<const int16_t*>(record + uint64_t(kFastGroup) * groups_per_block)[group];
+    decode_group_to<false>(reinterpret_cast<u32x4*>(stage + unit * kFastGroup), shift, bytes, lane);
+    if (unit % (2 * kv_heads) == 0 && lane == 0) index[b] = int32_t(b);
+}
+
+void launch_stage_history_2048(const uint8_t* records, const int32_t* ids, uint64_t record_bytes, uint32_t groups_per_block, uint32_t layer,
+                               uint32_t layers, uint32_t kv_heads, uint32_t blocks, uint16_t* stage, int32_t* index, hipStream_t stream) {
+    const uint64_t waves = uint64_t(blocks) * 2 * kv_heads;
+    const uint32_t grid = uint32_t((waves + kCodecWaves - 1) / kCodecWaves);
+    hipLaunchKernelGGL(stage_history_2048, dim3(grid), dim3(kWave * kCodecWaves), 0, stream, records, ids, record_bytes, groups_per_block, layer,
+                       layers, kv_heads, blocks, stage, index);
 }
 
 void launch_quantize_2048(const uint16_t* pool, const int32_t* ids, uint8_t* stage, uint32_t count, uint32_t groups_per_block,

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stdlib.h>
+#include <string.h>
 
 #include <stdexcept>
 #include <string>
@@ -533,11 +534,19 @@ namespace lk {
 // splits each tile's keys, at least 4 steps (128 keys) per split and at most kMaxKeySplits
 // splits, and merges the partials in prefill_merge. LAYOVER_PREFILL_SPLITS=n forces n
 // splits (tests), read per launch.
+//
+// FP8-record pools, given a workspace (lk_paged_prefill_split): the chunk's history is first
+// decoded, one layer, into a compact BF16 pool in the workspace (stage_history_2048: each
+// record byte read once, 2 bytes written), and the BF16 kernel runs on that. The FP8 form of
+// the LDS kernel converts every K/V tile in every workgroup that reads it instead, once per
+// 128-row tile. LAYOVER_PREFILL_FP8=direct keeps the direct FP8 kernel (tests), read per
+// launch; lk_paged_prefill, which has no workspace, always runs it.
 struct PrefillPlan {
     uint64_t row_tiles;
     uint32_t key_splits;
     uint32_t split_steps;
-    bool shared;  // the LDS kernel (the register-only one never splits)
+    bool shared;      // the LDS kernel (the register-only one never splits)
+    bool stage_fp8;   // FP8 pool decoded into the workspace first
 };
 
 // CUs of the current device, cached per device; 256 (MI355X) when no device answers, with the
@@ -575,6 +584,8 @@ PrefillPlan prefill_plan(const lk_prefill_shape& s) {
     p.key_splits = 1;
     p.split_steps = max_steps;
     if (!p.shared) return p;
+    const char* fp8_choice = getenv("LAYOVER_PREFILL_FP8");
+    p.stage_fp8 = s.kv_format == LK_FP8_RECORD && !(fp8_choice && strcmp(fp8_choice, "direct") == 0);
     uint32_t wanted = 0;
     if (const char* forced = getenv("LAYOVER_PREFILL_SPLITS")) {
         wanted = uint32_t(strtoul(forced, nullptr, 10));
@@ -593,11 +604,32 @@ PrefillPlan prefill_plan(const lk_prefill_shape& s) {
     return p;
 }
 
-uint64_t prefill_workspace(const lk_prefill_shape& s, const PrefillPlan& p) {
-    if (p.key_splits <= 1) return 0;
-    const uint64_t rows = uint64_t(s.tokens) * (s.query_heads / s.kv_heads);
-    return uint64_t(s.kv_heads) * rows * p.key_splits * (kDim + 2) * sizeof(float);
+// Workspace layout: [staged BF16 history | staged block index | split partials], each part
+// 256-byte aligned; parts the plan does not use are absent.
+struct PrefillWorkspace {
+    uint64_t stage_bytes, index_bytes, partial_bytes;
+    uint64_t total() const { return stage_bytes + index_bytes + partial_bytes; }
+};
+
+uint64_t round_up_256(uint64_t bytes) { return (bytes + 255) / 256 * 256; }
+
+uint64_t staged_block_bytes(const lk_prefill_shape& s) { return uint64_t(2) * s.kv_heads * kSlots * kDim * 2; }
+
+PrefillWorkspace prefill_workspace_parts(const lk_prefill_shape& s, const PrefillPlan& p) {
+    PrefillWorkspace w{};
+    if (p.stage_fp8) {
+        const uint64_t blocks = (uint64_t(s.start) + s.tokens + kSlots - 1) / kSlots;
+        w.stage_bytes = round_up_256(blocks * staged_block_bytes(s));
+        w.index_bytes = round_up_256(blocks * sizeof(int32_t));
+    }
+    if (p.key_splits > 1) {
+        const uint64_t rows = uint64_t(s.tokens) * (s.query_heads / s.kv_heads);
+        w.partial_bytes = uint64_t(s.kv_heads) * rows * p.key_splits * (kDim + 2) * sizeof(float);
+    }
+    return w;
 }
+
+uint64_t prefill_workspace(const lk_prefill_shape& s, const PrefillPlan& p) { return prefill_workspace_parts(s, p).total(); }
 
 void check_prefill(const lk_prefill_shape& s) {
     require(s.tokens > 0 && s.query_heads > 0 && s.kv_heads > 0 && s.layers > 0, "every prefill dimension must be positive");
@@ -627,9 +659,11 @@ void run_prefill(const lk_prefill_shape& s, const void* q, const void* pool, con
     if (!may_split) {
         p.key_splits = 1;
         p.split_steps = uint32_t((((end + kSlots - 1) / kSlots) + 1) / 2);
+        p.stage_fp8 = false;
     }
-    const uint64_t need = prefill_workspace(s, p);
-    require(need == 0 || (workspace != nullptr && workspace_bytes >= need && aligned(workspace, 4)),
+    const PrefillWorkspace parts = prefill_workspace_parts(s, p);
+    const uint64_t need = parts.total();
+    require(need == 0 || (workspace != nullptr && workspace_bytes >= need && aligned(workspace, 16)),
             "workspace smaller than lk_paged_prefill_workspace");
     const uint32_t groups = s.query_heads / s.kv_heads;
     const uint64_t rows = uint64_t(s.tokens) * groups;
@@ -652,9 +686,25 @@ void run_prefill(const lk_prefill_shape& s, const void* q, const void* pool, con
     a.scale_log2 = s.scale * kLog2e;
     a.key_splits = p.key_splits;
     a.split_steps = p.split_steps;
-    a.partial_acc = static_cast<float*>(workspace);
+    uint8_t* const space = static_cast<uint8_t*>(workspace);
+    a.partial_acc = p.key_splits > 1 ? reinterpret_cast<float*>(space + parts.stage_bytes + parts.index_bytes) : nullptr;
     a.partial_ml = p.key_splits > 1 ? a.partial_acc + uint64_t(s.kv_heads) * rows * p.key_splits * kDim : nullptr;
-    if (p.shared && s.kv_format == LK_BF16)
+    if (p.stage_fp8) {
+        // The history's blocks, this layer only, as a one-layer BF16 pool; the BF16 kernel then
+        // reads block b of it through index[b] = b.
+        const uint32_t blocks = uint32_t((end + kSlots - 1) / kSlots);
+        uint16_t* stage = reinterpret_cast<uint16_t*>(space);
+        int32_t* index = reinterpret_cast<int32_t*>(space + parts.stage_bytes);
+        const uint32_t groups_per_block = 2 * s.layers * s.kv_heads;
+        launch_stage_history_2048(static_cast<const uint8_t*>(pool), block_ids, block_bytes, groups_per_block, s.layer, s.layers, s.kv_heads,
+                                  blocks, stage, index, st);
+        a.pool = space;
+        a.block_ids = index;
+        a.layers = 1;
+        a.layer = 0;
+        a.block_bytes = staged_block_bytes(s);
+        hipLaunchKernelGGL(prefill_mfma_lds<LK_BF16>, dim3(uint32_t(grid)), dim3(kWave * kLdsWaves), 0, st, a);
+    } else if (p.shared && s.kv_format == LK_BF16)
         hipLaunchKernelGGL(prefill_mfma_lds<LK_BF16>, dim3(uint32_t(grid)), dim3(kWave * kLdsWaves), 0, st, a);
     else if (p.shared)
         hipLaunchKernelGGL(prefill_mfma_lds<LK_FP8_RECORD>, dim3(uint32_t(grid)), dim3(kWave * kLdsWaves), 0, st, a);

@@ -166,3 +166,25 @@ def test_prefill_split_plan_sizes_its_workspace(monkeypatch):
     assert lib.lk_paged_prefill_workspace(short) == 8 * 2048 * 55 * 130 * 4
     bad = _lib.PrefillShape(512, 8192, 30, 8, 128, 36, 16, 0, _lib.LK_BF16, _lib.LK_BF16, 1.0)
     assert lib.lk_paged_prefill_workspace(bad) == 0
+
+
+def test_fp8_prefill_workspace_holds_the_staged_history(monkeypatch):
+    """An FP8-record pool's history is staged as a one-layer BF16 pool (64 KiB a block at
+    Qwen3-4B's 8 KV heads) plus an int32 index, each part 256-byte aligned, ahead of any split
+    partials; LAYOVER_PREFILL_FP8=direct leaves only the partials."""
+    from layover_amd.kernels import _lib
+
+    lib = _lib.load()
+    fp8 = _lib.LK_FP8_RECORD
+    long_chunk = _lib.PrefillShape(2048, 30720, 32, 8, 128, 36, 16, 0, _lib.LK_BF16, fp8, 128**-0.5)
+    blocks = 32768 // 16
+    assert lib.lk_paged_prefill_workspace(long_chunk) == blocks * 65536 + blocks * 4
+    short = _lib.PrefillShape(512, 8192 + 5, 32, 8, 128, 36, 16, 0, _lib.LK_BF16, fp8, 128**-0.5)
+    blocks = -(-(8192 + 5 + 512) // 16)  # 545
+    index = -(-blocks * 4 // 256) * 256
+    monkeypatch.setenv("LAYOVER_PREFILL_SPLITS", "4")
+    assert lib.lk_paged_prefill_workspace(short) == blocks * 65536 + index + 8 * 2048 * 4 * 130 * 4
+    monkeypatch.setenv("LAYOVER_PREFILL_FP8", "direct")
+    assert lib.lk_paged_prefill_workspace(short) == 8 * 2048 * 4 * 130 * 4
+    monkeypatch.delenv("LAYOVER_PREFILL_SPLITS")
+    assert lib.lk_paged_prefill_workspace(long_chunk) == 0

@@ -64,16 +64,21 @@ def test_prefill_gqa_ratios(query_heads):
     assert_close(out, oracle.prefill_attention(q.float().cpu().numpy(), bits, 0, block_ids, 77, query_heads // 8))
 
 
+@pytest.mark.parametrize("path", ["staged", "direct"])
 @pytest.mark.parametrize("start,tokens", [(0, 24), (300, 90)])
-def test_prefill_reads_fp8_records(start, tokens):
+def test_prefill_reads_fp8_records(start, tokens, path, monkeypatch):
+    """FP8-record pools: the history staged as BF16 in the workspace, or read directly by the
+    FP8 form of the kernel (LAYOVER_PREFILL_FP8=direct)."""
     from layover_amd.kernels.hip_prefill import paged_prefill_attention_hip
+
+    monkeypatch.setenv("LAYOVER_PREFILL_FP8", path)
 
     end = start + tokens
     blocks = -(-end // 16)
     pool, state = make_pool(blocks, 2, 8, seed=7, fp8=True)
     block_ids = np.random.default_rng(8).permutation(blocks).astype(np.int32)
     q = torch.randn(32, tokens, 128, device="cuda").to(torch.bfloat16)
-    print(f"prefill fp8 start={start} tokens={tokens}", flush=True)
+    print(f"prefill fp8 {path} start={start} tokens={tokens}", flush=True)
     out = paged_prefill_attention_hip(q, pool, 1, torch.from_numpy(block_ids).cuda(), start, 4)
     torch.cuda.synchronize()
     assert_close(out, oracle.prefill_attention(q.float().cpu().numpy(), state, 1, block_ids, start, 4))
@@ -131,7 +136,7 @@ def test_prefill_refuses_what_it_cannot_run():
         paged_prefill_attention_hip(q.float(), pool, 0, ids, 0, 4)
 
 
-@pytest.mark.parametrize("kernel", ["lds", "register_only"])
+@pytest.mark.parametrize("kernel", ["staged", "lds", "register_only"])
 def test_prefill_fp8_tiny_groups_take_the_exact_decode(kernel, monkeypatch):
     """Groups scaled by 2^-114 get shifts below -117, where the hardware convert times
     2^shift could leave BF16's normal range; those blocks are decoded with the reference's
@@ -141,6 +146,7 @@ def test_prefill_fp8_tiny_groups_take_the_exact_decode(kernel, monkeypatch):
     from layover_amd.kernels.hip_prefill import paged_prefill_attention_hip
 
     monkeypatch.setenv("LAYOVER_PREFILL_KERNEL", "1" if kernel == "register_only" else "0")
+    monkeypatch.setenv("LAYOVER_PREFILL_FP8", "staged" if kernel == "staged" else "direct")
     blocks, layers = 8, 2
     rng = np.random.default_rng(21)
     values = rng.standard_normal((blocks, 2, layers, 8, 16, 128), dtype=np.float32)
@@ -164,7 +170,7 @@ def test_prefill_fp8_tiny_groups_take_the_exact_decode(kernel, monkeypatch):
 
 
 @pytest.mark.parametrize("splits", ["1", "3", "7"])
-@pytest.mark.parametrize("fp8", [False, True], ids=["bf16_pool", "fp8_pool"])
+@pytest.mark.parametrize("fp8", [False, True, "direct"], ids=["bf16_pool", "fp8_pool", "fp8_pool_direct"])
 @pytest.mark.parametrize("start,tokens", [(0, 37), (1000, 130), (4090, 7), (300, 90)])
 def test_split_keys_match_the_oracle(start, tokens, fp8, splits, monkeypatch):
     """Split-K: each tile's key steps spread over 1, 3 or 7 workgroups whose partials are
@@ -173,6 +179,7 @@ def test_split_keys_match_the_oracle(start, tokens, fp8, splits, monkeypatch):
     from layover_amd.kernels.hip_prefill import paged_prefill_attention_hip
 
     monkeypatch.setenv("LAYOVER_PREFILL_SPLITS", splits)
+    monkeypatch.setenv("LAYOVER_PREFILL_FP8", "direct" if fp8 == "direct" else "staged")
     end = start + tokens
     blocks = -(-end // 16)
     pool, state = make_pool(blocks, 2, 8, seed=tokens, fp8=fp8)
