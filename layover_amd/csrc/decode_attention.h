@@ -105,6 +105,7 @@ struct DecodeArgs {
     uint32_t splits;       // splits per sequence (grid)
     uint32_t bps;          // blocks per split
     uint32_t order;        // workgroup order, see decode_unit_of
+    uint32_t vector_combine;  // workspace and out aligned for combine_dim128's vector accesses
     uint64_t block_bytes;  // bytes from one pool block to the next
     float scale_log2;      // softmax scale * log2(e)
 };
@@ -619,8 +620,67 @@ __global__ __launch_bounds__(kWave) void decode_split_generic(DecodeArgs a) {
 // ---------------------------------------------------------------------------------------
 // Combine: out[seq, qh] = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
 
+// Combine for 128-dim heads and at most 64 splits (batch 1 at 32,768 tokens has 32): lane l
+// takes dims 4 (l % 32) .. +3 of the splits of parity l / 32, so every row load of the wave
+// (one 16-byte load per lane and split pair) goes out at once with the length and the (m, l)
+// pairs, and nothing waits on more than one round trip to memory. The two halves' sums meet
+// in one cross-half shuffle.
+template <int QF>
+__device__ __forceinline__ void combine_dim128(const DecodeArgs& a, void* out, uint32_t seq, uint32_t qh) {
+    const uint32_t lane = threadIdx.x;
+    const uint32_t quad = lane % 32, half = lane / 32;
+    const int32_t length = a.lengths[uint64_t(seq) * a.lengths_stride];
+    const uint64_t base = (uint64_t(seq) * a.query_heads + qh) * a.splits;
+    const float* ml = a.partial_ml + 2 * base;
+    const f32x4* acc = reinterpret_cast<const f32x4*>(a.partial_acc + base * kDim);
+    float lane_m = -INFINITY, lane_l = 0.0f;
+    if (lane < a.splits) {
+        lane_m = ml[2 * lane];
+        lane_l = ml[2 * lane + 1];
+    }
+    f32x4 rows[kWave / 2];
+#pragma unroll
+    for (uint32_t j = 0; j < kWave / 2; ++j) {
+        if (2 * j < a.splits) rows[j] = acc[uint64_t(min(2 * j + half, a.splits - 1)) * (kDim / 4) + quad];
+    }
+    const uint32_t used = (blocks_of(length, a.slots) + a.bps - 1) / a.bps;
+    float top = lane < used ? lane_m : -INFINITY;
+#pragma unroll
+    for (int mask = 32; mask >= 1; mask >>= 1) top = fmaxf(top, __shfl_xor(top, mask, kWave));
+    const float weight = lane < used ? merge_weight(lane_m, top) : 0.0f;
+    float total = lane < used ? lane_l * weight : 0.0f;
+#pragma unroll
+    for (int mask = 32; mask >= 1; mask >>= 1) total += __shfl_xor(total, mask, kWave);
+    f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (uint32_t j = 0; j < kWave / 2; ++j) {
+        if (2 * j >= a.splits) break;
+        const uint32_t s = 2 * j + half;
+        const float w = __shfl(weight, int(s), kWave);
+        // Splits past the used ones hold anything: selected away, never multiplied by zero.
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sum[i] = s < used ? fmaf(w, rows[j][i], sum[i]) : sum[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sum[i] += __shfl_xor(sum[i], 32, kWave);
+    if (half != 0) return;
+    const float inverse = 1.0f / total;
+    const uint64_t at = (uint64_t(seq) * a.query_heads + qh) * kDim + 4 * quad;
+    if constexpr (QF == LK_BF16) {
+        const uint32_t lo = uint32_t(to_bf16(sum[0] * inverse)) | (uint32_t(to_bf16(sum[1] * inverse)) << 16);
+        const uint32_t hi = uint32_t(to_bf16(sum[2] * inverse)) | (uint32_t(to_bf16(sum[3] * inverse)) << 16);
+        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(out) + at) = u32x2{lo, hi};
+    } else {
+        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(out) + at) = f32x4{sum[0] * inverse, sum[1] * inverse, sum[2] * inverse, sum[3] * inverse};
+    }
+}
+
 template <int QF>
 __global__ __launch_bounds__(kWave) void decode_combine(DecodeArgs a, void* out) {
+    if (a.vector_combine && a.head_dim == kDim && a.splits <= kWave) {
+        combine_dim128<QF>(a, out, blockIdx.x / a.query_heads, blockIdx.x % a.query_heads);
+        return;
+    }
     // Latency-bound at small batch (one wave per (sequence, query head), a few KiB each): every
     // load that does not depend on another is issued at once. The sequence's length, the splits'
     // (m, l) pairs and the first kChunk splits' rows all go out together; splits past the ones

@@ -518,6 +518,7 @@ LK_EXPORT int lk_paged_decode(const lk_decode_shape* shape, const void* q, const
         a.splits = g.splits;
         a.bps = g.bps;
         a.order = lk::env_order();
+        a.vector_combine = lk::aligned(workspace, 16) && lk::aligned(out, s.q_format == LK_BF16 ? 8 : 16);
         a.block_bytes = lk::pool_block_bytes(s);
         a.scale_log2 = s.scale * lk::kLog2e;
         lk::require(lk::aligned(pool, s.kv_format == LK_F32 ? 4 : (s.kv_format == LK_BF16 ? 2 : 1)), "misaligned pool");

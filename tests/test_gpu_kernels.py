@@ -450,3 +450,30 @@ def test_stream_probe_mix_moves_the_stated_bytes(ratio):
     assert bool((dst[dst_bytes // 4 :] == -7).all())
     with pytest.raises(_lib.KernelError):
         _lib.check(lib.lk_stream_probe_mix(src.data_ptr(), src_bytes, dst.data_ptr(), src_bytes, stream))
+
+
+@pytest.mark.parametrize("case", ["vector_combine", "unaligned_buffers", "over_64_splits"])
+def test_decode_combine_paths_match_the_oracle(hip_decode, case):
+    """The split merge has a vector form (128-dim heads, at most 64 splits, 16-byte aligned
+    workspace and out) and a general one. A workspace 4 bytes off 16-byte alignment and an out
+    2 bytes off take the general form; a 70,000-token row (69 splits) takes it too."""
+    lengths = [70000, 3] if case == "over_64_splits" else [5000, 17, 2100]
+    q, pool, table, lens = decode_case(lengths, layers=1, kv_heads=2, slots=16, head_dim=128, groups=4, seed=len(case))
+    expected = oracle.decode_attention(q, pool, 0, table, lens, 4)
+    q_gpu, pool_gpu = to_gpu_bf16(q), to_gpu_bf16(pool)
+    table_gpu, lens_gpu = torch.from_numpy(table).cuda(), torch.from_numpy(lens).cuda()
+    from layover_amd.kernels import _lib
+
+    shape = hip_decode.decode_shape(q_gpu, pool_gpu, 0, table_gpu, 4, lens_gpu)
+    need = int(_lib.load().lk_paged_decode_workspace(shape))
+    if case == "unaligned_buffers":
+        workspace = torch.empty(need + 16, dtype=torch.uint8, device="cuda")[4 : 4 + need]
+        out = torch.empty(q_gpu.numel() + 1, dtype=torch.bfloat16, device="cuda")[1:].view(q_gpu.shape)
+        assert workspace.data_ptr() % 16 == 4 and out.data_ptr() % 8 == 2
+    else:
+        workspace = torch.empty(need, dtype=torch.uint8, device="cuda")
+        out = torch.empty_like(q_gpu)
+    print(f"decode combine {case}: workspace {need} bytes", flush=True)
+    hip_decode.run_kernel(q_gpu, pool_gpu, 0, table_gpu, lens_gpu, 4, out, workspace)
+    torch.cuda.synchronize()
+    assert_close_to_oracle(out, expected, case)
