@@ -93,6 +93,11 @@ void launch_quantize_2048(const uint16_t* pool, const int32_t* ids, uint8_t* sta
                           uint32_t grid, hipStream_t stream);
 void launch_dequantize_2048(const uint8_t* stage, const int32_t* ids, uint16_t* pool, uint32_t count, uint32_t groups_per_block,
                             uint32_t grid, hipStream_t stream);
+// One token per row written into Qwen3-shaped FP8 records (16 slots x 128 dims, 16-byte
+// aligned records, k and v), the fast form of lk_fp8_append.
+void launch_append_2048(uint8_t* records, const int32_t* write_block, const int32_t* write_slot, uint32_t row_stride, uint32_t batch,
+                        const uint16_t* k, const uint16_t* v, uint32_t layer, uint32_t layers, uint32_t kv_heads, uint32_t grid,
+                        hipStream_t stream);
 // One layer of the FP8 records of blocks ids[0 .. blocks) decoded into a compact one-layer BF16
 // pool `stage` [blocks][2][kv_heads][16 x 128], with index[b] = b (the paged prefill's
 // FP8 path). Groups of 2,048 values; the records' shifts follow their codes.

@@ -276,74 +276,6 @@ __global__ __launch_bounds__(kWave* kCodecWaves) void append_groups(uint8_t* __r
 }
 
 
-// The same for Qwen3-shaped groups (16 slots x 128 dims, 16-byte aligned records, k and v):
-// lane l holds bytes 32l .. 32l+31 of the group, i.e. slot l/4 and dims 32(l%4) .. +31, in
-// registers from two 16-byte loads, so the group is read once and written once.
-__global__ __launch_bounds__(kWave* kCodecWaves) void append_groups_2048(uint8_t* __restrict__ records, const int32_t* __restrict__ write_block,
-                                                                       const int32_t* __restrict__ write_slot, uint32_t row_stride,
-                                                                       uint32_t batch, const uint16_t* __restrict__ k,
-                                                                       const uint16_t* __restrict__ v, uint32_t layer, uint32_t layers,
-                                                                       uint32_t kv_heads) {
-    constexpr uint32_t kDims = 128;
-    const uint32_t lane = threadIdx.x % kWave;
-    const uint64_t unit = uint64_t(blockIdx.x) * kCodecWaves + threadIdx.x / kWave;
-    if (unit >= uint64_t(batch) * 2 * kv_heads) return;
-    const uint32_t head = uint32_t(unit % kv_heads);
-    const uint32_t kind = uint32_t(unit / kv_heads % 2);
-    const uint32_t row = uint32_t(unit / (2ull * kv_heads));
-    const uint32_t groups_per_block = 2 * layers * kv_heads;
-    const uint64_t block_elems = uint64_t(kFastGroup) * groups_per_block;
-    const uint64_t record = block_elems + 2ull * groups_per_block;
-    const uint32_t g = (kind * layers + layer) * kv_heads + head;
-    uint8_t* base = records + uint64_t(uint32_t(write_block[uint64_t(row) * row_stride])) * record;
-    u32x4* codes = reinterpret_cast<u32x4*>(base + uint64_t(g) * kFastGroup) + 2 * lane;
-    int16_t* shift_at = reinterpret_cast<int16_t*>(base + block_elems + 2ull * g);
-    const uint32_t write = uint32_t(write_slot[uint64_t(row) * row_stride]);
-    const uint32_t slot = lane / 4;
-    const int32_t old_shift = *shift_at;
-
-    const u32x4 old[2] = {codes[0], codes[1]};
-    uint32_t pairs[16];  // the lane's 32 new BF16 values, two per word
-    if (slot < write) {
-#pragma unroll
-        for (int w = 0; w < 8; ++w) {
-            const uint32_t word = old[w / 4][w % 4];
-            pairs[2 * w] = decode_e4m3(word & 0xFFu, old_shift) | (decode_e4m3((word >> 8) & 0xFFu, old_shift) << 16);
-            pairs[2 * w + 1] = decode_e4m3((word >> 16) & 0xFFu, old_shift) | (decode_e4m3(word >> 24, old_shift) << 16);
-        }
-    } else if (slot == write) {
-        const u32x4* fresh = reinterpret_cast<const u32x4*>((kind == 0 ? k : v) + (uint64_t(row) * kv_heads + head) * kDims + 32 * (lane % 4));
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const u32x4 w = fresh[j];
-#pragma unroll
-            for (int x = 0; x < 4; ++x) pairs[4 * j + x] = w[x];
-        }
-    } else {
-#pragma unroll
-        for (int x = 0; x < 16; ++x) pairs[x] = 0u;
-    }
-    uint32_t key = 0;
-#pragma unroll
-    for (int x = 0; x < 16; ++x) {
-        const uint32_t lo = exponent_key(pairs[x] & 0xFFFFu), hi = exponent_key(pairs[x] >> 16);
-        key = lo > key ? lo : key;
-        key = hi > key ? hi : key;
-    }
-    const int32_t shift = shift_from_key(wave_max(key));
-    u32x4 out[2];
-#pragma unroll
-    for (int w = 0; w < 8; ++w) {
-        const uint32_t a = pairs[2 * w], b = pairs[2 * w + 1];
-        out[w / 4][w % 4] = encode_e4m3(a & 0xFFFFu, shift) | (encode_e4m3(a >> 16, shift) << 8) | (encode_e4m3(b & 0xFFFFu, shift) << 16) |
-                            (encode_e4m3(b >> 16, shift) << 24);
-    }
-    codes[0] = out[0];
-    codes[1] = out[1];
-    if (lane == 0) *shift_at = int16_t(shift);
-}
-
-
 // One token per sequence written into a BF16 pool (lk_kv_write): the reference's decode-time
 // pool assignment (model.py:139-140) as one launch. Thread t of a row copies 16 bytes: K for
 // the first kv_heads * head_dim / 8 threads, V for the rest.
@@ -465,9 +397,8 @@ LK_EXPORT int lk_fp8_append(void* records, const int32_t* write_block, const int
         const uint64_t record = uint64_t(slots) * head_dim * 2 * layers * kv_heads + 4ull * layers * kv_heads;
         if (slots * head_dim == lk::kFastGroup && head_dim == 128 && record % 16 == 0 && lk::aligned(records, 16) && lk::aligned(k, 16) &&
             lk::aligned(v, 16)) {
-            hipLaunchKernelGGL(lk::append_groups_2048, dim3(grid), dim3(lk::kWave * lk::kCodecWaves), 0, static_cast<hipStream_t>(stream),
-                               static_cast<uint8_t*>(records), write_block, write_slot, row_stride, batch, static_cast<const uint16_t*>(k),
-                               static_cast<const uint16_t*>(v), layer, layers, kv_heads);
+            lk::launch_append_2048(static_cast<uint8_t*>(records), write_block, write_slot, row_stride, batch, static_cast<const uint16_t*>(k),
+                                   static_cast<const uint16_t*>(v), layer, layers, kv_heads, grid, static_cast<hipStream_t>(stream));
             return;
         }
         hipLaunchKernelGGL(lk::append_groups, dim3(grid), dim3(lk::kWave * lk::kCodecWaves), 0, static_cast<hipStream_t>(stream),

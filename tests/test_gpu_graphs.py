@@ -56,6 +56,43 @@ def test_fp8_append_is_bit_exact_against_the_oracle(shape):
     assert np.array_equal(pool.records.cpu().numpy(), expected)
 
 
+def test_fp8_append_takes_the_exact_codec_where_the_converts_are_not_exact():
+    """Qwen3-shaped appends decode the old codes and encode the group with the hardware
+    converts only where those are exact. Rows here force every other case: old shifts below
+    -117 and above 119, a NaN code among the old values, new shifts below -126, and a BF16
+    subnormal in an otherwise finite group (flushed to signed zero either way)."""
+    shape = QWEN_LIKE
+    blocks, rows, layer = 6, 6, 4
+    rng = np.random.default_rng(9)
+    values = rng.standard_normal((blocks, 2, shape["layers"], 8, 16, 128), dtype=np.float32)
+    values[0] *= np.float32(2.0**-114)  # old shift -119: integer decode
+    values[1] = np.clip(values[1], -3.5, 3.5) * np.float32(2.0**126)  # old shift 120 (finite): integer decode
+    values[2, :, layer, :, 3, 5] = np.nan  # a NaN code among the old values
+    values[3] *= np.float32(2.0**-122)  # new shift -127: integer encode
+    bits = oracle.bf16_bits(values)
+    group_elems, groups = 16 * 128, 2 * shape["layers"] * 8
+    records = oracle.quantize_records(bits, list(range(blocks)), group_elems, groups).reshape(blocks, -1)
+    shifts = records[:, group_elems * groups :].copy().view(np.int16).reshape(blocks, 2, shape["layers"], 8)[:, :, layer]
+    assert (shifts[0] < -117).all() and (shifts[1] > 119).all() and (shifts[3] < -126).all()
+    k = oracle.bf16_bits(rng.standard_normal((rows, 8, 128), dtype=np.float32))
+    v = oracle.bf16_bits(rng.standard_normal((rows, 8, 128), dtype=np.float32))
+    for row, gain in ((0, 2.0**-114), (1, 2.0**126), (3, 2.0**-122)):
+        k[row] = oracle.bf16_bits(np.clip(rng.standard_normal((8, 128), dtype=np.float32), -3.5, 3.5) * np.float32(gain))
+        v[row] = oracle.bf16_bits(np.clip(rng.standard_normal((8, 128), dtype=np.float32), -3.5, 3.5) * np.float32(gain))
+    k[4, :, 7] = 0x0003  # BF16 subnormals in finite groups
+    v[4, :, 9] = 0x8001
+    write_blocks = np.arange(rows, dtype=np.int32) % blocks
+    write_slots = np.full(rows, 10, dtype=np.int32)
+    pool = fp8_pool(records, **shape)
+    print("append exact-codec cases", flush=True)
+    pool.write(torch.from_numpy(write_blocks).cuda(), torch.from_numpy(write_slots).cuda(), layer,
+               torch.from_numpy(k.view(np.int16)).cuda().view(torch.bfloat16), torch.from_numpy(v.view(np.int16)).cuda().view(torch.bfloat16))
+    expected = oracle.append_tokens(records, shape["layers"], 8, 16, 128, write_blocks, write_slots, layer, k, v)
+    got = pool.records.cpu().numpy()
+    for block in range(blocks):
+        assert np.array_equal(got[block], expected[block]), f"block {block}"
+
+
 def test_fp8_append_into_an_empty_block_equals_quantizing_the_token():
     shape = QWEN_LIKE
     group_elems, groups = shape["slots"] * shape["head_dim"], 2 * shape["layers"] * shape["kv_heads"]
