@@ -12,7 +12,7 @@
 // (lane (g, n): keys 4g..4g+3 of row n), an online softmax per row with the lazy 2^8 rescale,
 // and O += P V with v_mfma_f32_16x16x16_bf16 (lane (g, n): rows 4g..4g+3, dims 8n + e of
 // MFMA e). P enters the MFMA as one BF16 (not the decode kernel's hi + lo pair): relative
-// error about 2^-9 per weight, against the north-star tolerance of 1e-2. Keys past a row's
+// error at most 2^-8 per weight, against the north-star tolerance of 1e-2. Keys past a row's
 // limit score -inf; V of slots at or past the chunk's end is zeroed, since those slots can
 // hold anything (0 * NaN is NaN).
 // Workgroups: 4 waves = 64 rows. Launch order: KV head fastest, and the heaviest row tiles

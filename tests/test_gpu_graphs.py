@@ -153,7 +153,8 @@ def decode_reference(pool_bits, q, tables_rows, groups):
 def weighted_mean_abs_v(q, pool_bits, layer, table, lengths, groups):
     """Per output, the attention-weighted mean of |v| (the same attention over V with its sign
     bits cleared): an FP8 pool's weights enter the matrix cores as single BF16s, relative
-    error at most 2^-9, so the output may err by 2^-9 of this."""
+    error at most 2^-8 (8 significand bits), so the output may err by 2^-8 of this. Seeded runs
+    of the strided test below reached 1.19 times a 2^-9 allowance (a 3-key row)."""
     magnitudes = pool_bits.copy()
     magnitudes[:, 1] &= 0x7FFF
     return oracle.decode_attention(q, magnitudes, layer, table, lengths, groups)
@@ -162,7 +163,7 @@ def weighted_mean_abs_v(q, pool_bits, layer, table, lengths, groups):
 def assert_close(got, reference, rounding=None):
     got = got.float().cpu().numpy().astype(np.float64)
     # BF16 output rounding plus FP32 accumulation, as in the other decode tests.
-    allowed = 2.0**-8 * np.abs(reference) + 1e-3 + (0.0 if rounding is None else 2.0**-9 * rounding)
+    allowed = 2.0**-8 * np.abs(reference) + 1e-3 + (0.0 if rounding is None else 2.0**-8 * rounding)
     assert np.all(np.abs(got - reference) <= allowed), np.abs(got - reference).max()
 
 
@@ -277,7 +278,8 @@ def test_decode_reads_packed_row_columns_by_stride(fp8):
     else:
         pool = torch.from_numpy(bits.view(np.int16)).cuda().view(torch.bfloat16)
         state = bits
-    q = torch.randn(4, 32, 128, device="cuda").to(torch.bfloat16)
+    # Seeded: this q gave the largest error of 3,000 seeds (1.19 times a 2^-9 weight allowance).
+    q = torch.randn(4, 32, 128, device="cuda", generator=torch.Generator(device="cuda").manual_seed(2442)).to(torch.bfloat16)
     strided, contiguous = torch.empty_like(q), torch.empty_like(q)
     print(f"strided decode fp8={fp8}", flush=True)
     hip_decode.run_kernel(q, pool, 20, packed[:, 3:], packed[:, 2], 4, strided)

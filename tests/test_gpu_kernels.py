@@ -222,8 +222,8 @@ def to_gpu_bf16(bits):
 
 def weighted_mean_abs_v(q, pool_bits, layer, table, lengths, groups):
     """Per output, the attention-weighted mean of |v|: the same attention over V with its
-    sign bits cleared. A kernel that rounds each weight to BF16 (relative error at most 2^-9)
-    errs by at most 2^-9 of this."""
+    sign bits cleared. A kernel that rounds each weight to BF16 (8 significand bits: relative
+    error at most 2^-8, reached for significands just above 1) errs by at most 2^-8 of this."""
     magnitudes = pool_bits.copy()
     magnitudes[:, 1] &= 0x7FFF
     return oracle.decode_attention(q, magnitudes, layer, table, lengths, groups)
@@ -236,7 +236,7 @@ def assert_close_to_oracle(out, expected, what="", weight_rounding=None):
     # |v| where the kernel feeds the weights to the matrix cores as single BF16s (FP8 pools).
     allowed = np.abs(expected) * 2.0**-8 + 1e-3
     if weight_rounding is not None:
-        allowed = allowed + 2.0**-9 * weight_rounding
+        allowed = allowed + 2.0**-8 * weight_rounding
     error = np.abs(got - expected)
     assert np.isfinite(got).all(), what
     assert (error <= allowed).all(), f"{what}: max error {error.max():.3g} at {np.unravel_index(error.argmax(), error.shape)}"
@@ -346,7 +346,7 @@ def test_decode_fp8_pool_with_extreme_shifts_uses_the_exact_decode(fp8, hip_deco
     out = hip_decode.paged_decode_attention_hip(to_gpu_bf16(q), fp8_pool, layers - 1, torch.from_numpy(table).cuda(), torch.from_numpy(lens).cuda(), 2)
     got = out.double().cpu().numpy()
     assert np.isfinite(got).all()
-    rounding = 2.0**-9 * weighted_mean_abs_v(q, dequantized, layers - 1, table, lens, 2) if layers == 4 else 0.0
+    rounding = 2.0**-8 * weighted_mean_abs_v(q, dequantized, layers - 1, table, lens, 2) if layers == 4 else 0.0
     assert (np.abs(got - expected) <= np.abs(expected) * 2.0**-7 + rounding + 2.0**-126).all()
 
 
