@@ -252,7 +252,9 @@ def swap_bench(args, device, pool_blocks: int, cache):
         # A bounded spin first, so every launch and event below is queued before the stream
         # reaches them: a pause of the host thread (one of 32 ms was seen) then cannot fall
         # inside a launch's event window.
-        torch.cuda._sleep(200_000_000)
+        spin = getattr(torch.cuda, "_sleep", None)  # torch's test helper: a kernel that spins for n cycles
+        if spin is not None:
+            spin(200_000_000)
         for _ in range(args.kernel_repeats):
             for index, (out_ids, in_ids) in enumerate(segments):
                 stage = stages[index % len(stages)]
