@@ -165,6 +165,18 @@ int lk_fp8_append(void* records, const int32_t* write_block, const int32_t* writ
                   const void* k, const void* v, uint32_t layer, uint32_t layers, uint32_t kv_heads, uint32_t slots,
                   uint32_t head_dim, void* stream);
 
+/* lk_kv_write (BF16 pool) or lk_fp8_append (FP8 records) of each row's new token into layer
+ * shape->layer, then lk_paged_decode of that layer, as one decode launch where the shape
+ * allows (the workgroups that read a row's last block write its token first). No counterpart
+ * in the reference, whose decode step writes the pool and then attends (layover/model.py:
+ * 139-141); for small-batch steps, which are bound by launches. The write position must be
+ * the row's last token: write_block[b*write_stride] = table[b][(lengths[b] - 1) / slots] and
+ * write_slot[b*write_stride] = (lengths[b] - 1) % slots, as PagedKVCache.decode_rows packs
+ * them; it is not checked. Rows must name distinct blocks. Other shapes run the two launches. */
+int lk_paged_decode_append(const lk_decode_shape* shape, const void* q, void* pool, const int32_t* table, const int32_t* lengths,
+                           const int32_t* write_block, const int32_t* write_slot, uint32_t write_stride, const void* k,
+                           const void* v, void* out, void* workspace, uint64_t workspace_bytes, void* stream);
+
 /* Measurement support, no reference counterpart: stream `bytes` (a multiple of 16, 16-byte
  * aligned) from `src`, copying to `dst`, or only reading when dst is null (then `sink`, one
  * device uint32, is written only if the data hash to a value chosen never to occur). This is

@@ -108,6 +108,14 @@ struct DecodeArgs {
     uint32_t vector_combine;  // workspace and out aligned for combine_dim128's vector accesses
     uint64_t block_bytes;  // bytes from one pool block to the next
     float scale_log2;      // softmax scale * log2(e)
+    // Fused decode-time write (lk_paged_decode_append; null write_block: none): row b's new
+    // token, k_new/v_new [batch, kv_heads, head_dim] BF16, goes to slot write_slot[b] of block
+    // write_block[b] (rows write_stride int32 apart), which must hold the row's last token.
+    const int32_t* write_block;
+    const int32_t* write_slot;
+    uint32_t write_stride;
+    const uint16_t* k_new;
+    const uint16_t* v_new;
 };
 
 __device__ __forceinline__ uint32_t blocks_of(int32_t length, uint32_t slots) { return (uint32_t(length) + slots - 1) / slots; }
@@ -289,6 +297,36 @@ __global__ __launch_bounds__(kWave* kDecodeWaves) void decode_split_mfma(DecodeA
     const uint64_t k_offset = head_tile * tile_bytes + (uint64_t(n) * kDim + MfmaTile<KV>::kGroupDims * g) * kElem;
     const uint64_t v_offset = (uint64_t(a.layers) * a.kv_heads + head_tile) * tile_bytes + (uint64_t(4 * g) * kDim + 8 * n) * kElem;
     const uint64_t block_elems = uint64_t(2) * a.layers * a.kv_heads * kSlots * kDim;  // FP8: shifts follow the data
+
+    // Fused decode-time write: the workgroups of the split holding the row's last block write
+    // the new token of their KV head (wave 0 K, wave 1 V; an FP8 group is re-encoded whole)
+    // before any wave loads that block. The token is the row's last, so no other split reads
+    // its block. The row's K/V rows are read only here, after the write, so the workgroup
+    // fences and barrier are all the ordering needed.
+    if (a.write_block != nullptr && first + count == nblocks) {
+        if (wave < 2) {
+            const uint32_t kind = wave;
+            const uint32_t block = uint32_t(a.write_block[uint64_t(seq) * a.write_stride]);
+            const uint32_t slot = uint32_t(a.write_slot[uint64_t(seq) * a.write_stride]);
+            const uint16_t* fresh = (kind == 0 ? a.k_new : a.v_new) + (uint64_t(seq) * a.kv_heads + kv_head) * kDim;
+            uint8_t* base = const_cast<uint8_t*>(a.pool) + uint64_t(block) * a.block_bytes;  // the pool is written only here
+            const uint64_t group = (uint64_t(kind) * a.layers + a.layer) * a.kv_heads + kv_head;
+            if constexpr (KV == LK_BF16) {
+                if (lane < 16) {
+                    const u32x4 w = reinterpret_cast<const u32x4*>(fresh)[lane];
+                    reinterpret_cast<u32x4*>(base + (group * kSlots + slot) * kDim * kElem)[lane] = w;
+                }
+            } else {
+                u32x4 row[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) row[j] = reinterpret_cast<const u32x4*>(fresh + 32 * (lane % 4))[j];
+                append_group_2048(base + group * kFastGroup, reinterpret_cast<int16_t*>(base + block_elems + 2 * group), slot, row, lane);
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __syncthreads();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    }
 
     // The block ids (and FP8 shifts) of this wave's units, one unit per lane (at most 64:
     // blocks per split <= 256), held before any tile is loaded and read back with v_readlane,

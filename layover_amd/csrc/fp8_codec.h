@@ -85,6 +85,101 @@ __device__ __forceinline__ uint32_t wave_max(uint32_t value) {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float codec_f32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float codec_pow2(int32_t e) { return __uint_as_float(uint32_t(e + 127) << 23); }
+
+// Both halves of a BF16 pair with subnormals replaced by signed zero (fp8.py:114), so the
+// hardware convert below gives the reference's bytes whatever the FP32 denormal mode.
+__device__ __forceinline__ uint32_t flush_bf16_pair(uint32_t pair) {
+    pair = (pair & 0x7F80u) == 0 ? (pair & 0xFFFF8000u) : pair;
+    return (pair & 0x7F800000u) == 0 ? (pair & 0x8000FFFFu) : pair;
+}
+
+// One token written into a Qwen3-shaped group of FP8 records (16 slots x 128 dims, 2,048
+// codes at `group`, its shift at `shift_at`), by one wave: lane l holds bytes 32l .. 32l+31
+// (slot l/4, dims 32(l%4) .. +31), so the group is read once and written once. Element e
+// becomes the old value decoded at the old shift for slots before `write`, the new BF16 value
+// (`fresh`: the lane's 32 values of the new token's row, dims 32(l%4) .. +31) at it, and zero
+// after it; the group is re-encoded at the shift of those values (fp8.py:86-137). Decode and
+// encode take the hardware converts where they are exact (as the record kernels do), else the
+// reference's integer codec.
+__device__ __forceinline__ void append_group_2048(uint8_t* group, int16_t* shift_at, uint32_t write, const u32x4 (&fresh)[4], uint32_t lane) {
+    u32x4* codes = reinterpret_cast<u32x4*>(group) + 2 * lane;
+    const uint32_t slot = lane / 4;
+    const u32x4 old[2] = {codes[0], codes[1]};
+    const int32_t old_shift = *shift_at;
+
+    // The old values (lanes before the write slot): a NaN code anywhere among them, or a shift
+    // whose products could leave BF16's normal range, sends the wave to the integer decode.
+    uint32_t nan_flags = 0;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) nan_flags |= (old[w / 4][w % 4] & 0x7F7F7F7Fu) + 0x01010101u;
+    const bool exact_decode = __any(slot < write && (nan_flags & 0x80808080u) != 0) || old_shift < -117 || old_shift > 119;
+    uint32_t pairs[16];  // the lane's 32 new BF16 values, two per word
+    if (slot < write) {
+        if (!exact_decode) {
+            const float scale = codec_pow2(old_shift);
+#pragma unroll
+            for (int w = 0; w < 8; ++w) {
+                const int word = int(old[w / 4][w % 4]);
+                const codec_f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(word, false);
+                const codec_f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(word, true);
+                pairs[2 * w] = __builtin_amdgcn_perm(__float_as_uint(lo.y * scale), __float_as_uint(lo.x * scale), 0x07060302u);
+                pairs[2 * w + 1] = __builtin_amdgcn_perm(__float_as_uint(hi.y * scale), __float_as_uint(hi.x * scale), 0x07060302u);
+            }
+        } else {
+#pragma unroll
+            for (int w = 0; w < 8; ++w) {
+                const uint32_t word = old[w / 4][w % 4];
+                pairs[2 * w] = decode_e4m3(word & 0xFFu, old_shift) | (decode_e4m3((word >> 8) & 0xFFu, old_shift) << 16);
+                pairs[2 * w + 1] = decode_e4m3((word >> 16) & 0xFFu, old_shift) | (decode_e4m3(word >> 24, old_shift) << 16);
+            }
+        }
+    } else if (slot == write) {
+#pragma unroll
+        for (int x = 0; x < 16; ++x) pairs[x] = fresh[x / 4][x % 4];
+    } else {
+#pragma unroll
+        for (int x = 0; x < 16; ++x) pairs[x] = 0u;
+    }
+
+    // Shift of the new values, and whether any is infinite or NaN (exponent field all ones).
+    uint32_t key = 0, flags = 0;
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+        const uint32_t lo = exponent_key(pairs[x] & 0xFFFFu), hi = exponent_key(pairs[x] >> 16);
+        key = lo > key ? lo : key;
+        key = hi > key ? hi : key;
+        flags |= (pairs[x] & 0x7F807F80u) + 0x00800080u;
+    }
+    const int32_t shift = shift_from_key(wave_max(key));
+    const bool nonfinite = __any((flags & 0x80008000u) != 0);
+    u32x4 out[2];
+    if (!nonfinite && shift >= -126) {
+        // value * 2^-shift is exact for a normal BF16 value and stays below 2^8; the convert
+        // rounds to nearest even. Subnormal inputs are flushed first; products below FP32's
+        // normal range round to zero codes either way.
+        const float scale = codec_pow2(-shift);
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+            const uint32_t a = flush_bf16_pair(pairs[2 * w]), b = flush_bf16_pair(pairs[2 * w + 1]);
+            int p = __builtin_amdgcn_cvt_pk_fp8_f32(__uint_as_float(a << 16) * scale, __uint_as_float(a & 0xFFFF0000u) * scale, 0, false);
+            p = __builtin_amdgcn_cvt_pk_fp8_f32(__uint_as_float(b << 16) * scale, __uint_as_float(b & 0xFFFF0000u) * scale, p, true);
+            out[w / 4][w % 4] = uint32_t(p);
+        }
+    } else {
+#pragma unroll
+        for (int w = 0; w < 8; ++w) {
+            const uint32_t a = pairs[2 * w], b = pairs[2 * w + 1];
+            out[w / 4][w % 4] = encode_e4m3(a & 0xFFFFu, shift) | (encode_e4m3(a >> 16, shift) << 8) |
+                                (encode_e4m3(b & 0xFFFFu, shift) << 16) | (encode_e4m3(b >> 16, shift) << 24);
+        }
+    }
+    codes[0] = out[0];
+    codes[1] = out[1];
+    if (lane == 0) *shift_at = int16_t(shift);
+}
 
 // Qwen3-shaped groups (2048 values, 16-byte aligned records) run the kernels of
 // fp8_records.hip; these launch them on `stream`.

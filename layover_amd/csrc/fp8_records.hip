@@ -275,13 +275,8 @@ __global__ __launch_bounds__(kWave* kCodecWaves) void stage_history_2048(const u
 }
 
 // One token per row written into Qwen3-shaped records (lk_fp8_append): one wave per (row,
-// kind, KV head) group, lane l holding bytes 32l .. 32l+31 of the group (slot l/4, dims
-// 32(l%4) .. +31), so the group is read once and written once. Element e of the group becomes
-// the old value decoded at the old shift for slots before the write slot, the new BF16 value at
-// it, and zero after it; the group is re-encoded at the shift of those values (fp8.py:86-137).
-// The new token's load needs only the row and goes out with the write position's; the old
-// codes and shift follow. Decode and encode take the hardware converts under the same
-// conditions as the record kernels above (exact there), else the reference's integer codec.
+// kind, KV head) group, running append_group_2048. The new token's loads need only the row
+// and go out with the write position's; the old codes and shift follow.
 __global__ __launch_bounds__(kWave* kCodecWaves) void append_groups_2048(uint8_t* __restrict__ records, const int32_t* __restrict__ write_block,
                                                                        const int32_t* __restrict__ write_slot, uint32_t row_stride,
                                                                        uint32_t batch, const uint16_t* __restrict__ k,
@@ -294,7 +289,6 @@ __global__ __launch_bounds__(kWave* kCodecWaves) void append_groups_2048(uint8_t
     const uint32_t head = uint32_t(unit % kv_heads);
     const uint32_t kind = uint32_t(unit / kv_heads % 2);
     const uint32_t row = uint32_t(unit / (2ull * kv_heads));
-    const uint32_t slot = lane / 4;
 
     const u32x4* fresh_at = reinterpret_cast<const u32x4*>((kind == 0 ? k : v) + (uint64_t(row) * kv_heads + head) * kDims + 32 * (lane % 4));
     u32x4 fresh[4];
@@ -308,77 +302,7 @@ __global__ __launch_bounds__(kWave* kCodecWaves) void append_groups_2048(uint8_t
     const uint64_t record = block_elems + 2ull * groups_per_block;
     const uint32_t g = (kind * layers + layer) * kv_heads + head;
     uint8_t* base = records + uint64_t(block) * record;
-    u32x4* codes = reinterpret_cast<u32x4*>(base + uint64_t(g) * kFastGroup) + 2 * lane;
-    int16_t* shift_at = reinterpret_cast<int16_t*>(base + block_elems + 2ull * g);
-    const u32x4 old[2] = {codes[0], codes[1]};
-    const int32_t old_shift = *shift_at;
-
-    // The old values (lanes before the write slot): a NaN code anywhere among them, or a shift
-    // whose products could leave BF16's normal range, sends the wave to the integer decode.
-    uint32_t nan_flags = 0;
-#pragma unroll
-    for (int w = 0; w < 8; ++w) nan_flags |= (old[w / 4][w % 4] & 0x7F7F7F7Fu) + 0x01010101u;
-    const bool exact_decode = __any(slot < write && (nan_flags & 0x80808080u) != 0) || old_shift < -117 || old_shift > 119;
-    uint32_t pairs[16];  // the lane's 32 new BF16 values, two per word
-    if (slot < write) {
-        if (!exact_decode) {
-            const float scale = power_of_two(old_shift);
-#pragma unroll
-            for (int w = 0; w < 8; ++w) {
-                const int word = int(old[w / 4][w % 4]);
-                const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(word, false);
-                const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(word, true);
-                pairs[2 * w] = __builtin_amdgcn_perm(__float_as_uint(lo.y * scale), __float_as_uint(lo.x * scale), 0x07060302u);
-                pairs[2 * w + 1] = __builtin_amdgcn_perm(__float_as_uint(hi.y * scale), __float_as_uint(hi.x * scale), 0x07060302u);
-            }
-        } else {
-#pragma unroll
-            for (int w = 0; w < 8; ++w) {
-                const uint32_t word = old[w / 4][w % 4];
-                pairs[2 * w] = decode_e4m3(word & 0xFFu, old_shift) | (decode_e4m3((word >> 8) & 0xFFu, old_shift) << 16);
-                pairs[2 * w + 1] = decode_e4m3((word >> 16) & 0xFFu, old_shift) | (decode_e4m3(word >> 24, old_shift) << 16);
-            }
-        }
-    } else if (slot == write) {
-#pragma unroll
-        for (int x = 0; x < 16; ++x) pairs[x] = fresh[x / 4][x % 4];
-    } else {
-#pragma unroll
-        for (int x = 0; x < 16; ++x) pairs[x] = 0u;
-    }
-
-    // Shift of the new values, and whether any is infinite or NaN (exponent field all ones).
-    uint32_t key = 0, flags = 0;
-#pragma unroll
-    for (int x = 0; x < 16; ++x) {
-        const uint32_t lo = exponent_key(pairs[x] & 0xFFFFu), hi = exponent_key(pairs[x] >> 16);
-        key = lo > key ? lo : key;
-        key = hi > key ? hi : key;
-        flags |= (pairs[x] & 0x7F807F80u) + 0x00800080u;
-    }
-    const int32_t shift = shift_from_key(wave_max(key));
-    const bool nonfinite = __any((flags & 0x80008000u) != 0);
-    u32x4 out[2];
-    if (!nonfinite && shift >= -126) {
-        const float scale = power_of_two(-shift);
-#pragma unroll
-        for (int w = 0; w < 8; ++w) {
-            const uint32_t a = pairs[2 * w], b = pairs[2 * w + 1];
-            int p = __builtin_amdgcn_cvt_pk_fp8_f32(__uint_as_float(a << 16) * scale, __uint_as_float(a & 0xFFFF0000u) * scale, 0, false);
-            p = __builtin_amdgcn_cvt_pk_fp8_f32(__uint_as_float(b << 16) * scale, __uint_as_float(b & 0xFFFF0000u) * scale, p, true);
-            out[w / 4][w % 4] = uint32_t(p);
-        }
-    } else {
-#pragma unroll
-        for (int w = 0; w < 8; ++w) {
-            const uint32_t a = pairs[2 * w], b = pairs[2 * w + 1];
-            out[w / 4][w % 4] = encode_e4m3(a & 0xFFFFu, shift) | (encode_e4m3(a >> 16, shift) << 8) |
-                                (encode_e4m3(b & 0xFFFFu, shift) << 16) | (encode_e4m3(b >> 16, shift) << 24);
-        }
-    }
-    codes[0] = out[0];
-    codes[1] = out[1];
-    if (lane == 0) *shift_at = int16_t(shift);
+    append_group_2048(base + uint64_t(g) * kFastGroup, reinterpret_cast<int16_t*>(base + block_elems + 2ull * g), write, fresh, lane);
 }
 
 void launch_append_2048(uint8_t* records, const int32_t* write_block, const int32_t* write_slot, uint32_t row_stride, uint32_t batch,

@@ -417,45 +417,92 @@ LK_EXPORT uint64_t lk_paged_decode_workspace(const lk_decode_shape* shape) {
     return lk::workspace_bytes(*shape);
 }
 
+namespace lk {
+
+struct TokenWrite {
+    const int32_t* write_block;
+    const int32_t* write_slot;
+    uint32_t stride;
+    const void* k;
+    const void* v;
+};
+
+void run_decode(const lk_decode_shape& s, const void* q, const void* pool, const int32_t* table, const int32_t* lengths, void* out,
+                void* workspace, uint64_t workspace_bytes, const TokenWrite* write, hipStream_t st) {
+    check_shape(s);
+    require(q && pool && table && lengths && out && workspace, "null q, pool, table, lengths, out or workspace");
+    require(workspace_bytes >= ::lk::workspace_bytes(s), "workspace smaller than lk_paged_decode_workspace");
+    require(aligned(workspace, 4), "workspace must be 4-byte aligned");
+    const Geometry g = geometry(s, pool);
+    DecodeArgs a{};
+    a.q = q;
+    a.pool = static_cast<const uint8_t*>(pool);
+    a.table = table;
+    a.lengths = lengths;
+    a.partial_acc = static_cast<float*>(workspace);
+    a.partial_ml = a.partial_acc + uint64_t(s.batch) * s.query_heads * g.splits * s.head_dim;
+    a.batch = s.batch;
+    a.query_heads = s.query_heads;
+    a.kv_heads = s.kv_heads;
+    a.head_dim = s.head_dim;
+    a.layers = s.layers;
+    a.slots = s.slots;
+    a.layer = s.layer;
+    a.table_width = s.table_width;
+    a.table_stride = s.table_stride != 0 ? s.table_stride : s.table_width;
+    a.lengths_stride = s.lengths_stride != 0 ? s.lengths_stride : 1;
+    require(a.table_stride >= s.table_width, "table_stride is smaller than table_width");
+    a.groups = s.query_heads / s.kv_heads;
+    a.splits = g.splits;
+    a.bps = g.bps;
+    a.order = env_order();
+    a.vector_combine = aligned(workspace, 16) && aligned(out, s.q_format == LK_BF16 ? 8 : 16);
+    a.block_bytes = pool_block_bytes(s);
+    a.scale_log2 = s.scale * kLog2e;
+    require(aligned(pool, s.kv_format == LK_F32 ? 4 : (s.kv_format == LK_BF16 ? 2 : 1)), "misaligned pool");
+    if (write != nullptr) {
+        require(write->write_block && write->write_slot && write->k && write->v, "null write rows, k or v");
+        require(write->stride > 0, "write_stride must be positive");
+        require(s.kv_format == LK_BF16 || s.kv_format == LK_FP8_RECORD, "a fused write needs a BF16 or FP8-record pool");
+        require(aligned(write->k, 16) && aligned(write->v, 16), "k and v must be 16-byte aligned");
+        if (g.fast) {
+            a.write_block = write->write_block;
+            a.write_slot = write->write_slot;
+            a.write_stride = write->stride;
+            a.k_new = static_cast<const uint16_t*>(write->k);
+            a.v_new = static_cast<const uint16_t*>(write->v);
+        } else {
+            // Shapes the matrix-core kernel does not take: the write as its own launch first.
+            const int status = s.kv_format == LK_BF16
+                                   ? lk_kv_write(const_cast<void*>(pool), write->write_block, write->write_slot, write->stride, s.batch, write->k,
+                                                 write->v, s.layer, s.layers, s.kv_heads, s.slots, s.head_dim, st)
+                                   : lk_fp8_append(const_cast<void*>(pool), write->write_block, write->write_slot, write->stride, s.batch,
+                                                   write->k, write->v, s.layer, s.layers, s.kv_heads, s.slots, s.head_dim, st);
+            if (status == LK_ERR_INVALID) throw Invalid(last_error);
+            if (status != LK_OK) throw std::runtime_error(last_error);
+        }
+    }
+    if (s.q_format == LK_BF16) launch_decode<LK_BF16>(a, g, s.kv_format, out, st);
+    else launch_decode<LK_F32>(a, g, s.kv_format, out, st);
+}
+
+}  // namespace lk
+
 LK_EXPORT int lk_paged_decode(const lk_decode_shape* shape, const void* q, const void* pool, const int32_t* table,
                               const int32_t* lengths, void* out, void* workspace, uint64_t workspace_bytes, void* stream) {
     return lk::guarded([&] {
         lk::require(shape != nullptr, "null shape");
-        const lk_decode_shape& s = *shape;
-        lk::check_shape(s);
-        lk::require(q && pool && table && lengths && out && workspace, "null q, pool, table, lengths, out or workspace");
-        lk::require(workspace_bytes >= lk::workspace_bytes(s), "workspace smaller than lk_paged_decode_workspace");
-        lk::require(lk::aligned(workspace, 4), "workspace must be 4-byte aligned");
-        const lk::Geometry g = lk::geometry(s, pool);
-        lk::DecodeArgs a{};
-        a.q = q;
-        a.pool = static_cast<const uint8_t*>(pool);
-        a.table = table;
-        a.lengths = lengths;
-        a.partial_acc = static_cast<float*>(workspace);
-        a.partial_ml = a.partial_acc + uint64_t(s.batch) * s.query_heads * g.splits * s.head_dim;
-        a.batch = s.batch;
-        a.query_heads = s.query_heads;
-        a.kv_heads = s.kv_heads;
-        a.head_dim = s.head_dim;
-        a.layers = s.layers;
-        a.slots = s.slots;
-        a.layer = s.layer;
-        a.table_width = s.table_width;
-        a.table_stride = s.table_stride != 0 ? s.table_stride : s.table_width;
-        a.lengths_stride = s.lengths_stride != 0 ? s.lengths_stride : 1;
-        lk::require(a.table_stride >= s.table_width, "table_stride is smaller than table_width");
-        a.groups = s.query_heads / s.kv_heads;
-        a.splits = g.splits;
-        a.bps = g.bps;
-        a.order = lk::env_order();
-        a.vector_combine = lk::aligned(workspace, 16) && lk::aligned(out, s.q_format == LK_BF16 ? 8 : 16);
-        a.block_bytes = lk::pool_block_bytes(s);
-        a.scale_log2 = s.scale * lk::kLog2e;
-        lk::require(lk::aligned(pool, s.kv_format == LK_F32 ? 4 : (s.kv_format == LK_BF16 ? 2 : 1)), "misaligned pool");
-        auto st = static_cast<hipStream_t>(stream);
-        if (s.q_format == LK_BF16) lk::launch_decode<LK_BF16>(a, g, s.kv_format, out, st);
-        else lk::launch_decode<LK_F32>(a, g, s.kv_format, out, st);
+        lk::run_decode(*shape, q, pool, table, lengths, out, workspace, workspace_bytes, nullptr, static_cast<hipStream_t>(stream));
+    });
+}
+
+LK_EXPORT int lk_paged_decode_append(const lk_decode_shape* shape, const void* q, void* pool, const int32_t* table, const int32_t* lengths,
+                                     const int32_t* write_block, const int32_t* write_slot, uint32_t write_stride, const void* k,
+                                     const void* v, void* out, void* workspace, uint64_t workspace_bytes, void* stream) {
+    return lk::guarded([&] {
+        lk::require(shape != nullptr, "null shape");
+        const lk::TokenWrite write{write_block, write_slot, write_stride, k, v};
+        lk::run_decode(*shape, q, pool, table, lengths, out, workspace, workspace_bytes, &write, static_cast<hipStream_t>(stream));
     });
 }
 

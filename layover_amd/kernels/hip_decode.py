@@ -230,6 +230,34 @@ def run_kernel(q, pool, layer, block_table, lengths, kv_groups, out, workspace=N
     )
 
 
+def run_kernel_append(q, pool, layer, block_table, lengths, kv_groups, write_blocks, write_slots, k, v, out, workspace=None) -> None:
+    """write_tokens (BF16 pool) or Fp8KVPool.write (FP8 records) of each row's new token into
+    `layer`, then run_kernel of that layer, as one decode launch where the shape allows
+    (lk_paged_decode_append). The write position must be the row's last token, as the first
+    two columns of PagedKVCache.decode_rows give it; that is not checked. Rows must name
+    distinct blocks. Enqueued on the current stream."""
+    _check_layout(q, block_table, lengths, out)
+    if _is_fp8(pool):
+        storage, layers, kv_heads, head_dim = pool.records, pool.layers, pool.kv_heads, pool.head_dim
+    else:
+        if pool.dtype != torch.bfloat16:
+            raise ValueError("a fused write needs a BF16 or FP8-record pool")
+        storage, layers, kv_heads, head_dim = pool, pool.shape[2], pool.shape[3], pool.shape[5]
+    batch = _check_token_write(storage.device, layers, kv_heads, head_dim, write_blocks, write_slots, layer, k, v)
+    if batch != q.shape[0]:
+        raise ValueError("one written token per decode row")
+    lib = _lib.load()
+    shape = decode_shape(q, pool, layer, block_table, kv_groups, lengths)
+    need = int(lib.lk_paged_decode_workspace(shape))
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=q.device)
+    _lib.check(
+        lib.lk_paged_decode_append(shape, q.data_ptr(), storage.data_ptr(), block_table.data_ptr(), lengths.data_ptr(),
+                                   write_blocks.data_ptr(), write_slots.data_ptr(), write_blocks.stride(0), k.data_ptr(), v.data_ptr(),
+                                   out.data_ptr(), workspace.data_ptr(), workspace.numel(), _lib.current_stream(q.device))
+    )
+
+
 def _launch(q, pool, layer, block_table, lengths, kv_groups) -> torch.Tensor:
     q = q.contiguous()
     block_table = block_table.to(torch.int32).contiguous()

@@ -5,8 +5,10 @@ attention work per layer is tens of microseconds, so issuing each layer's launch
 Python sets the pace; a graph records a step's launches once and replays them as one. The
 reference captures its whole model step; the model is outside this package, so the unit
 captured here is the data path's share of a step: for every layer, the new token's K/V write
-into the pool (model.py:139-140: hip_decode.write_tokens, or Fp8KVPool.write for an
-FP8-resident pool) and paged decode attention over the block table.
+into the pool (model.py:139-140: what hip_decode.write_tokens, or Fp8KVPool.write for an
+FP8-resident pool, does) and paged decode attention over the block table, as one launch
+(hip_decode.run_kernel_append: the workgroups that read a row's last block write its token
+first).
 
 As in the reference, each captured batch size gets fixed input tensors: one packed int32
 block of rows (write block, write slot, length, block table of fixed width, as
@@ -104,11 +106,10 @@ class DecodeAttentionGraphs:
         out = torch.empty(self.layers, size, self.query_heads, self.head_dim, dtype=self.q.dtype, device=self.q.device)
         workspace = self._workspaces[size]
         for layer in range(self.layers):
-            if isinstance(self.pool, Fp8KVPool):
-                self.pool.write(blocks, slots, layer, self.k_new[layer, :size], self.v_new[layer, :size])
-            else:
-                hip_decode.write_tokens(self.pool, blocks, slots, layer, self.k_new[layer, :size], self.v_new[layer, :size])
-            hip_decode.run_kernel(self.q[layer, :size], self.pool, layer, table, lengths, self.groups, out[layer], workspace)
+            # The token write and attention as one launch (the write position is the row's last
+            # token, as decode_rows packs it): lk_paged_decode_append.
+            hip_decode.run_kernel_append(self.q[layer, :size], self.pool, layer, table, lengths, self.groups, blocks, slots,
+                                         self.k_new[layer, :size], self.v_new[layer, :size], out[layer], workspace)
         return out
 
     def replay(self, size: int) -> torch.Tensor:

@@ -309,3 +309,53 @@ def test_bf16_token_write_equals_the_reference_assignment():
     write_tokens(cache.pool, packed[:, 0], packed[:, 1], 17, k, v)
     torch.cuda.synchronize()
     assert torch.equal(cache.pool.view(torch.int16), expected.view(torch.int16))
+
+
+@pytest.mark.parametrize("fp8", [False, True], ids=["bf16_pool", "fp8_pool"])
+def test_fused_write_and_decode_equal_the_two_launches(fp8):
+    """lk_paged_decode_append against write_tokens / Fp8KVPool.write followed by run_kernel on
+    a copy of the same pool: the pools' bytes and the outputs are identical. Rows end at a
+    block's first slot, its last slot, mid-block, and past a split boundary (64 blocks)."""
+    from layover_amd.config import ModelConfig
+    from layover_amd.kernels import hip_decode
+    from layover_amd.kv.paged_cache import BlockTable, PagedKVCache
+
+    blocks = 160
+    cache = PagedKVCache(ModelConfig.qwen3_4b(), blocks, fill=False)
+    rng = np.random.default_rng(13)
+    bits = oracle.bf16_bits(rng.standard_normal(cache.pool.shape, dtype=np.float32))
+    ids = rng.permutation(blocks).tolist()
+    lengths = [1, 16, 17, 130, 65 * 16 + 3]
+    tables, at = [], 0
+    for n in lengths:
+        need = -(-n // 16)
+        tables.append(BlockTable(ids[at : at + need], n))
+        at += need
+    packed = cache.decode_rows(tables).cuda()
+    blocks_col, slots_col, lengths_col, table = packed[:, 0], packed[:, 1], packed[:, 2], packed[:, 3:]
+    if fp8:
+        records = oracle.quantize_records(bits, list(range(blocks)), 16 * 128, 576).reshape(blocks, -1)
+        fused_pool, split_pool = fp8_pool(records, **QWEN_LIKE), fp8_pool(records.copy(), **QWEN_LIKE)
+    else:
+        fused_pool = torch.from_numpy(bits.view(np.int16)).cuda().view(torch.bfloat16)
+        split_pool = fused_pool.clone()
+    batch = len(lengths)
+    g = torch.Generator(device="cuda").manual_seed(4)
+    q = torch.randn(batch, 32, 128, device="cuda", generator=g).to(torch.bfloat16)
+    k = (torch.randn(batch, 8, 128, device="cuda", generator=g) * 3).to(torch.bfloat16)
+    v = torch.randn(batch, 8, 128, device="cuda", generator=g).to(torch.bfloat16)
+    layer = 35
+    fused, separate = torch.empty_like(q), torch.empty_like(q)
+    print(f"fused write+decode fp8={fp8}", flush=True)
+    hip_decode.run_kernel_append(q, fused_pool, layer, table, lengths_col, 4, blocks_col, slots_col, k, v, fused)
+    if fp8:
+        split_pool.write(blocks_col, slots_col, layer, k, v)
+    else:
+        hip_decode.write_tokens(split_pool, blocks_col, slots_col, layer, k, v)
+    hip_decode.run_kernel(q, split_pool, layer, table, lengths_col, 4, separate)
+    torch.cuda.synchronize()
+    if fp8:
+        assert torch.equal(fused_pool.records, split_pool.records)
+    else:
+        assert torch.equal(fused_pool.view(torch.int16), split_pool.view(torch.int16))
+    assert torch.equal(fused.view(torch.int16), separate.view(torch.int16))
