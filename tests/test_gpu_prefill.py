@@ -84,13 +84,25 @@ def test_prefill_reads_fp8_records(start, tokens, path, monkeypatch):
     assert_close(out, oracle.prefill_attention(q.float().cpu().numpy(), state, 1, block_ids, start, 4))
 
 
-def test_slots_past_the_chunk_end_never_reach_the_output():
+@pytest.mark.parametrize("form", ["bf16", "fp8_staged", "fp8_direct"])
+def test_slots_past_the_chunk_end_never_reach_the_output(form, monkeypatch):
+    """NaN in every slot past the chunk's end (FP8 records: NaN codes there) never reaches the
+    output, on a BF16 pool and on FP8 records staged as BF16 or read directly."""
+    from layover_amd.kernels.hip_decode import Fp8KVPool
     from layover_amd.kernels.hip_prefill import paged_prefill_attention_hip
 
+    monkeypatch.setenv("LAYOVER_PREFILL_FP8", "direct" if form == "fp8_direct" else "staged")
     pool, bits = make_pool(4, 1, 8, seed=11)
     poisoned = bits.copy()
     poisoned[3, :, 0, :, 9:] = 0x7FC0  # NaN in every slot of the last block past token 57
-    pool.copy_(torch.from_numpy(poisoned.view(np.int16)).cuda().view(torch.bfloat16))
+    if form == "bf16":
+        pool.copy_(torch.from_numpy(poisoned.view(np.int16)).cuda().view(torch.bfloat16))
+    else:
+        records = oracle.quantize_records(poisoned, list(range(4)), 16 * 128, 16)
+        bits = np.zeros_like(poisoned)
+        oracle.dequantize_records(records, list(range(4)), bits, 16 * 128, 16)
+        bits[3, :, 0, :, 9:] = 0  # the oracle reads only tokens before the end
+        pool = Fp8KVPool(torch.from_numpy(records.reshape(4, -1)).cuda(), 1, 8, 16, 128)
     block_ids = np.array([2, 0, 1, 3], dtype=np.int32)
     q = torch.randn(32, 20, 128, device="cuda").to(torch.bfloat16)
     out = paged_prefill_attention_hip(q, pool, 0, torch.from_numpy(block_ids).cuda(), 37, 4)
