@@ -359,3 +359,47 @@ def test_fused_write_and_decode_equal_the_two_launches(fp8):
     else:
         assert torch.equal(fused_pool.view(torch.int16), split_pool.view(torch.int16))
     assert torch.equal(fused.view(torch.int16), separate.view(torch.int16))
+
+
+@pytest.mark.parametrize("fp8", [False, True], ids=["bf16_pool", "fp8_pool"])
+def test_fused_write_on_other_shapes_runs_the_two_launches(fp8):
+    """A shape the matrix-core kernel does not take (micro: head_dim 24) runs the write and
+    decode launches one after the other inside lk_paged_decode_append: same bytes and outputs
+    as calling them separately."""
+    from layover_amd.config import ModelConfig
+    from layover_amd.kernels import hip_decode
+    from layover_amd.kv.paged_cache import BlockTable, PagedKVCache
+
+    cache = PagedKVCache(ModelConfig.micro(), 12, fill=False)
+    layers, kv_heads, slots, head_dim = cache.pool.shape[2], cache.pool.shape[3], cache.pool.shape[4], cache.pool.shape[5]
+    rng = np.random.default_rng(21)
+    bits = oracle.bf16_bits(rng.standard_normal(cache.pool.shape, dtype=np.float32))
+    tables = [BlockTable([3, 7], 20), BlockTable([5], 1), BlockTable([1, 2, 9], 48)]
+    packed = cache.decode_rows(tables).cuda()
+    if fp8:
+        groups = 2 * layers * kv_heads
+        records = oracle.quantize_records(bits, list(range(12)), slots * head_dim, groups).reshape(12, -1)
+        fused_pool = fp8_pool(records, layers, kv_heads, slots, head_dim)
+        split_pool = fp8_pool(records.copy(), layers, kv_heads, slots, head_dim)
+    else:
+        fused_pool = torch.from_numpy(bits.view(np.int16)).cuda().view(torch.bfloat16)
+        split_pool = fused_pool.clone()
+    query_heads = 2 * kv_heads
+    g = torch.Generator(device="cuda").manual_seed(6)
+    q = torch.randn(3, query_heads, head_dim, device="cuda", generator=g).to(torch.bfloat16)
+    k = torch.randn(3, kv_heads, head_dim, device="cuda", generator=g).to(torch.bfloat16)
+    v = torch.randn(3, kv_heads, head_dim, device="cuda", generator=g).to(torch.bfloat16)
+    fused, separate = torch.empty_like(q), torch.empty_like(q)
+    layer = layers - 1
+    hip_decode.run_kernel_append(q, fused_pool, layer, packed[:, 3:], packed[:, 2], 2, packed[:, 0], packed[:, 1], k, v, fused)
+    if fp8:
+        split_pool.write(packed[:, 0], packed[:, 1], layer, k, v)
+    else:
+        hip_decode.write_tokens(split_pool, packed[:, 0], packed[:, 1], layer, k, v)
+    hip_decode.run_kernel(q, split_pool, layer, packed[:, 3:], packed[:, 2], 2, separate)
+    torch.cuda.synchronize()
+    if fp8:
+        assert torch.equal(fused_pool.records, split_pool.records)
+    else:
+        assert torch.equal(fused_pool.view(torch.int16), split_pool.view(torch.int16))
+    assert torch.equal(fused.view(torch.int16), separate.view(torch.int16))
