@@ -56,7 +56,7 @@ HBM_PEAK_GBS = 8000.0
 # as 4 GiB, and its 4 GiB copy as 4 GiB of WRITE_SIZE. Per full 113-record launch:
 # 2 x 130,221 + 130,686 KiB measured against 390,636 KiB algorithmic.
 QUANTIZE_TRAFFIC_RATIO = 1.0012
-L4_FP8_SWAP_MS = 67.0  # README.md:27, :115 of the reference (NVIDIA L4)
+L4_FP8_SWAP_MS = 67.0  # the reference's published FP8 swap out+in at 8,192 tokens on an NVIDIA L4 (README.md:27, :115)
 QWEN = dict(layers=36, kv_heads=8, query_heads=32, slots=16, head_dim=128)
 POOL_BYTES = 12 << 30
 

@@ -18,7 +18,7 @@ Recompute time needs the model's prefill, which this package does not have; `--m
 these swap coefficients into a cost model JSON the reference's own sweep produced, keeping
 its recompute_s_coef, so CostModel.from_json(path, transfer="native") loads the result.
 
-    python -m layover_amd.kv.swap_costs --device cuda --out gpurun_out/swap_costs
+    python -m layover_amd.kv.swap_costs --device cuda --out swap_costs
 """
 
 from __future__ import annotations
