@@ -149,6 +149,26 @@ def test_token_write_and_prefill_arguments_are_checked_without_a_gpu():
         hip_prefill.paged_prefill_attention_hip(q, pool, 0, ids[:1], 10, 4)
 
 
+def test_fused_write_and_decode_arguments_are_checked_without_a_gpu():
+    """run_kernel_append checks the decode layout and the token write from metadata alone,
+    before any launch, so it refuses CPU tensors, an FP32 pool and a row count mismatch here."""
+    from layover_amd.kernels import hip_decode
+
+    cache = PagedKVCache(ModelConfig.micro(), 12, fill=False)
+    packed = cache.decode_rows([BlockTable([3, 7], 20), BlockTable([5], 1)])
+    table, lengths, blocks, slots = packed[:, 3:], packed[:, 2], packed[:, 0], packed[:, 1]
+    q = torch.zeros(2, 4, 24, dtype=torch.bfloat16)
+    k = torch.zeros(2, 2, 24, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="one GPU"):
+        hip_decode.run_kernel_append(q, cache.pool, 1, table, lengths, 2, blocks, slots, k, k, q.clone())
+    with pytest.raises(ValueError, match="BF16 or FP8-record pool"):
+        hip_decode.run_kernel_append(q, cache.pool.float(), 1, table, lengths, 2, blocks, slots, k, k, q.clone())
+    with pytest.raises(ValueError, match="int32"):
+        hip_decode.run_kernel_append(q, cache.pool, 1, table, lengths, 2, blocks.long(), slots, k, k, q.clone())
+    with pytest.raises(ValueError, match="layer"):
+        hip_decode.run_kernel_append(q, cache.pool, 2, table, lengths, 2, blocks, slots, k, k, q.clone())
+
+
 def test_prefill_split_plan_sizes_its_workspace(monkeypatch):
     """Short chunks against long histories split their keys; full-GPU chunks do not. The plan
     assumes 256 CUs when no device answers (as here)."""
