@@ -658,46 +658,71 @@ __global__ __launch_bounds__(kWave) void decode_split_generic(DecodeArgs a) {
 // ---------------------------------------------------------------------------------------
 // Combine: out[seq, qh] = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
 
-// Combine for 128-dim heads and at most 64 splits (batch 1 at 32,768 tokens has 32): lane l
-// takes dims 4 (l % 32) .. +3 of the splits of parity l / 32, so every row load of the wave
-// (one 16-byte load per lane and split pair) goes out at once with the length and the (m, l)
-// pairs, and nothing waits on more than one round trip to memory. The two halves' sums meet
-// in one cross-half shuffle.
-template <int QF>
+// Combine for 128-dim heads and at most 128 splits (batch 1 at 32,768 tokens has 32): lane l
+// takes dims 4 (l % 32) .. +3 of the splits of parity l / 32. Every row load of the first 64
+// splits goes out at once with the length and the (m, l) pairs, so up to 64 splits nothing
+// waits on more than one round trip to memory; splits 64-127 are a second batch of loads. The
+// two halves' sums meet in one cross-half shuffle.
+constexpr uint32_t kVectorSplits = 2 * kWave;
+template <int QF, bool kTwoPages>
 __device__ __forceinline__ void combine_dim128(const DecodeArgs& a, void* out, uint32_t seq, uint32_t qh) {
+    constexpr uint32_t kPages = kTwoPages ? 2 : 1;
     const uint32_t lane = threadIdx.x;
     const uint32_t quad = lane % 32, half = lane / 32;
     const int32_t length = a.lengths[uint64_t(seq) * a.lengths_stride];
     const uint64_t base = (uint64_t(seq) * a.query_heads + qh) * a.splits;
     const float* ml = a.partial_ml + 2 * base;
     const f32x4* acc = reinterpret_cast<const f32x4*>(a.partial_acc + base * kDim);
-    float lane_m = -INFINITY, lane_l = 0.0f;
-    if (lane < a.splits) {
-        lane_m = ml[2 * lane];
-        lane_l = ml[2 * lane + 1];
+    // Lane l holds the (m, l) of splits l and 64 + l.
+    float lane_m[kPages], lane_l[kPages];
+#pragma unroll
+    for (uint32_t page = 0; page < kPages; ++page) {
+        lane_m[page] = -INFINITY;
+        lane_l[page] = 0.0f;
+        if (page * kWave + lane < a.splits) {
+            lane_m[page] = ml[2 * (page * kWave + lane)];
+            lane_l[page] = ml[2 * (page * kWave + lane) + 1];
+        }
     }
     f32x4 rows[kWave / 2];
+    auto load_page = [&](uint32_t page) __attribute__((always_inline)) {
 #pragma unroll
-    for (uint32_t j = 0; j < kWave / 2; ++j) {
-        if (2 * j < a.splits) rows[j] = acc[uint64_t(min(2 * j + half, a.splits - 1)) * (kDim / 4) + quad];
-    }
+        for (uint32_t j = 0; j < kWave / 2; ++j) {
+            const uint32_t s = page * kWave + 2 * j;
+            if (s < a.splits) rows[j] = acc[uint64_t(min(s + half, a.splits - 1)) * (kDim / 4) + quad];
+        }
+    };
+    load_page(0);
     const uint32_t used = (blocks_of(length, a.slots) + a.bps - 1) / a.bps;
-    float top = lane < used ? lane_m : -INFINITY;
+    float top = -INFINITY;
+#pragma unroll
+    for (uint32_t page = 0; page < kPages; ++page) top = page * kWave + lane < used ? fmaxf(top, lane_m[page]) : top;
 #pragma unroll
     for (int mask = 32; mask >= 1; mask >>= 1) top = fmaxf(top, __shfl_xor(top, mask, kWave));
-    const float weight = lane < used ? merge_weight(lane_m, top) : 0.0f;
-    float total = lane < used ? lane_l * weight : 0.0f;
+    float weight[kPages], total = 0.0f;
+#pragma unroll
+    for (uint32_t page = 0; page < kPages; ++page) {
+        weight[page] = page * kWave + lane < used ? merge_weight(lane_m[page], top) : 0.0f;
+        total += page * kWave + lane < used ? lane_l[page] * weight[page] : 0.0f;
+    }
 #pragma unroll
     for (int mask = 32; mask >= 1; mask >>= 1) total += __shfl_xor(total, mask, kWave);
     f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto add_page = [&](uint32_t page) __attribute__((always_inline)) {
 #pragma unroll
-    for (uint32_t j = 0; j < kWave / 2; ++j) {
-        if (2 * j >= a.splits) break;
-        const uint32_t s = 2 * j + half;
-        const float w = __shfl(weight, int(s), kWave);
-        // Splits past the used ones hold anything: selected away, never multiplied by zero.
+        for (uint32_t j = 0; j < kWave / 2; ++j) {
+            const uint32_t s = page * kWave + 2 * j + half;
+            if (page * kWave + 2 * j >= a.splits) break;
+            const float w = __shfl(weight[page], int(2 * j + half), kWave);
+            // Splits past the used ones hold anything: selected away, never multiplied by zero.
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sum[i] = s < used ? fmaf(w, rows[j][i], sum[i]) : sum[i];
+            for (int i = 0; i < 4; ++i) sum[i] = s < used ? fmaf(w, rows[j][i], sum[i]) : sum[i];
+        }
+    };
+    add_page(0);
+    if constexpr (kTwoPages) {
+        load_page(1);
+        add_page(1);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) sum[i] += __shfl_xor(sum[i], 32, kWave);
@@ -713,12 +738,17 @@ __device__ __forceinline__ void combine_dim128(const DecodeArgs& a, void* out, u
     }
 }
 
+// The vector combine as its own kernel per page count, so each keeps its own register count.
+template <int QF, bool kTwoPages>
+__global__ __launch_bounds__(kWave) void decode_combine_vector(DecodeArgs a, void* out) {
+    combine_dim128<QF, kTwoPages>(a, out, blockIdx.x / a.query_heads, blockIdx.x % a.query_heads);
+}
+
+__host__ inline bool vector_combine_fits(const DecodeArgs& a) { return a.vector_combine && a.head_dim == kDim && a.splits <= kVectorSplits; }
+
 template <int QF>
 __global__ __launch_bounds__(kWave) void decode_combine(DecodeArgs a, void* out) {
-    if (a.vector_combine && a.head_dim == kDim && a.splits <= kWave) {
-        combine_dim128<QF>(a, out, blockIdx.x / a.query_heads, blockIdx.x % a.query_heads);
-        return;
-    }
+
     // Latency-bound at small batch (one wave per (sequence, query head), a few KiB each): every
     // load that does not depend on another is issued at once. The sequence's length, the splits'
     // (m, l) pairs and the first kChunk splits' rows all go out together; splits past the ones

@@ -185,7 +185,10 @@ void launch_decode(const DecodeArgs& a, const Geometry& g, int kv, void* out, hi
         else if (kv == LK_F32) hipLaunchKernelGGL((decode_split_generic<LK_F32, QF>), dim3(uint32_t(grid)), dim3(kWave), 0, stream, a);
         else hipLaunchKernelGGL((decode_split_generic<LK_FP8_RECORD, QF>), dim3(uint32_t(grid)), dim3(kWave), 0, stream, a);
     }
-    hipLaunchKernelGGL((decode_combine<QF>), dim3(a.batch * a.query_heads), dim3(kWave), 0, stream, a, out);
+    const dim3 grid(a.batch * a.query_heads);
+    if (!vector_combine_fits(a)) hipLaunchKernelGGL((decode_combine<QF>), grid, dim3(kWave), 0, stream, a, out);
+    else if (a.splits <= kWave) hipLaunchKernelGGL((decode_combine_vector<QF, false>), grid, dim3(kWave), 0, stream, a, out);
+    else hipLaunchKernelGGL((decode_combine_vector<QF, true>), grid, dim3(kWave), 0, stream, a, out);
 }
 
 // Streaming probes. Each wave moves one chunk, once: kRead 16-byte words per lane from `src`

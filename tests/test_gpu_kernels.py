@@ -452,12 +452,13 @@ def test_stream_probe_mix_moves_the_stated_bytes(ratio):
         _lib.check(lib.lk_stream_probe_mix(src.data_ptr(), src_bytes, dst.data_ptr(), src_bytes, stream))
 
 
-@pytest.mark.parametrize("case", ["vector_combine", "unaligned_buffers", "over_64_splits"])
+@pytest.mark.parametrize("case", ["vector_combine", "unaligned_buffers", "over_64_splits", "over_128_splits"])
 def test_decode_combine_paths_match_the_oracle(hip_decode, case):
-    """The split merge has a vector form (128-dim heads, at most 64 splits, 16-byte aligned
-    workspace and out) and a general one. A workspace 4 bytes off 16-byte alignment and an out
-    2 bytes off take the general form; a 70,000-token row (69 splits) takes it too."""
-    lengths = [70000, 3] if case == "over_64_splits" else [5000, 17, 2100]
+    """The split merge has a vector form (128-dim heads, at most 128 splits, 16-byte aligned
+    workspace and out) and a general one. A 70,000-token row (69 splits) takes the vector
+    form's second batch of loads; a workspace 4 bytes off 16-byte alignment and an out 2 bytes
+    off, or a 140,000-token row (137 splits), take the general form."""
+    lengths = {"over_64_splits": [70000, 3], "over_128_splits": [140000, 3]}.get(case, [5000, 17, 2100])
     q, pool, table, lens = decode_case(lengths, layers=1, kv_heads=2, slots=16, head_dim=128, groups=4, seed=len(case))
     expected = oracle.decode_attention(q, pool, 0, table, lens, 4)
     q_gpu, pool_gpu = to_gpu_bf16(q), to_gpu_bf16(pool)
