@@ -21,9 +21,11 @@ Also measured in the same run (extra keys of the JSON line):
   overlap     configs[4]: decode steps while 2,048 blocks swap out and back in
   decode_distinct  configs[2] on a ~78 GB pool whose rows share no block
   hbm_probe   lk_stream_probe read and copy rates and lk_stream_probe_mix at the FP8 kernels' read/write mixes: the measured HBM ceilings
-  cpu_baseline  the oracle's C restatement of the FP8 swap arithmetic on a bounded sample,
-              single-threaded on the host cores
-  cpu_reference_config1  configs[0] on the reference's own host library (oracle/_ref)
+  swap_bf16   the same 512 blocks swapped raw (gather kernel + DMA), byte-exact
+  cpu_baseline  the oracle's C restatement of the FP8 swap arithmetic on all 512 blocks, in
+              threads on the host cores; its records are compared with the GPU payload
+  cpu_config1  configs[0]: 64 of 4,096 BF16 blocks out and back on the host libraries (the
+              reference's own, built from its sources into oracle/_ref, and this package's)
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-decode] [--skip-cpu]
 """
@@ -37,14 +39,6 @@ import os
 import sys
 import time
 from pathlib import Path
-
-# Hardware queues per process for HIP streams (read once, when HIP starts). With HIP's default of
-# 4 the transfer engine's copy stream and the FP8 kernels' side stream were dealt the same
-# queue, so each segment's quantize waited for the previous segment's copy to the host; with 8
-# they overlap (measured on MI355X: FP8 swap-out 11.22 -> 10.92 ms, swap-in 11.03 -> 10.84 ms).
-# A larger value already set is kept.
-if int(os.environ.get("GPU_MAX_HW_QUEUES", "4") or "4") < 8:
-    os.environ["GPU_MAX_HW_QUEUES"] = "8"
 
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
@@ -211,6 +205,9 @@ def swap_bench(args, device, pool_blocks: int, cache):
     reference = np.zeros_like(bits)
     oracle.dequantize_records(expected, list(range(len(sample))), reference, layout.group_elems, layout.groups_per_block)
     parity = bool(np.array_equal(got, expected) and np.array_equal(restored, reference))
+    gpu_records = memory[: args.blocks * layout.record_bytes].copy()  # checked in full against the CPU leg
+    # The source blocks as they were quantized (later legs write into the pool).
+    source_bits = cache.pool[torch.tensor(src, device=device)].view(torch.int16).cpu().numpy().view(np.uint16).reshape(len(src), -1)
     backend.free(payload)
     if not parity:
         raise SystemExit("FP8 swap is not bit-exact against the oracle: refusing to report a number")
@@ -246,9 +243,9 @@ def swap_bench(args, device, pool_blocks: int, cache):
     per = backend.engine.staging_bytes // layout.record_bytes
     segments = [(torch.tensor(src[i : i + per], dtype=torch.int32, device=device), torch.tensor(dst[i : i + per], dtype=torch.int32, device=device))
                 for i in range(0, len(src), per)]
-    stages = backend._stages
+    stages = backend.stages
     quantize_timer.recording = dequantize_timer.recording = True
-    with torch.cuda.stream(backend._stream):
+    with torch.cuda.stream(backend.kernel_stream):
         # A bounded spin first, so every launch and event below is queued before the stream
         # reaches them: a pause of the host thread (one of 32 ms was seen) then cannot fall
         # inside a launch's event window.
@@ -274,6 +271,67 @@ def swap_bench(args, device, pool_blocks: int, cache):
         "parity_sample_records": len(sample),
         "segments_per_direction": math.ceil(args.blocks / ((args.staging_mib << 20) // layout.record_bytes)),
         "engine_memcpys": stats["memcpys"],
+        "source_bits": source_bits,
+        "gpu_records": gpu_records,
+    }
+
+
+def bf16_swap_bench(args, device, pool_blocks: int, cache) -> dict:
+    """The same 512 blocks swapped as raw BF16 (lt_out_gather / lt_in_scatter: gather kernel,
+    DMA per 128 MiB segment, two slots), the reference's 109 ms path on an L4 (README.md:27)."""
+    import numpy as np
+    import torch
+
+    from layover_amd.kv.transfer import NativeBackend
+
+    rng = np.random.default_rng(1)
+    chosen = rng.permutation(pool_blocks)[: 2 * args.blocks]
+    src = [int(i) for i in chosen[: args.blocks]]
+    dst = [int(i) for i in chosen[args.blocks :]]
+    backend = NativeBackend(device, staging_bytes=args.staging_mib << 20, num_staging=2, ids_capacity=1 << 20)
+    backend.prepare(cache, fp8=False)
+    try:
+        def step():
+            out = backend.start_out(cache, src)
+            out.wait()
+            backend.start_in(cache, dst, out.payload).wait()
+            return out.payload
+
+        for _ in range(args.warmup):
+            backend.free(step())
+        payload = step()
+        source = cache.pool[torch.tensor(src, device=device)].view(torch.uint8).reshape(-1).cpu().numpy()
+        landed = cache.pool[torch.tensor(dst, device=device)].view(torch.uint8).reshape(-1).cpu().numpy()
+        parity = bool(np.array_equal(payload.memory.numpy(), source) and np.array_equal(landed, source))
+        backend.free(payload)
+        if not parity:
+            raise SystemExit("BF16 swap is not byte-exact: refusing to report a number")
+        out_ms, in_ms = [], []
+        torch.cuda.synchronize()
+        for _ in range(args.steps):
+            t0 = time.perf_counter()
+            out = backend.start_out(cache, src)
+            out.wait()
+            t1 = time.perf_counter()
+            backend.start_in(cache, dst, out.payload).wait()
+            t2 = time.perf_counter()
+            backend.free(out.payload)
+            out_ms.append((t1 - t0) * 1e3)
+            in_ms.append((t2 - t1) * 1e3)
+        stats = backend.engine.stats()
+    finally:
+        backend.close()
+    each_way = args.blocks * cache.block_bytes
+    total_ms = sum(out_ms) / len(out_ms) + sum(in_ms) / len(in_ms)
+    return {
+        "ms_per_step": round(total_ms, 3),
+        "out_ms": round(sorted(out_ms)[len(out_ms) // 2], 3),
+        "in_ms": round(sorted(in_ms)[len(in_ms) // 2], 3),
+        "bytes_each_way": each_way,
+        "round_trip_gbs": round(2 * each_way / (total_ms * 1e-3) / 1e9, 2),
+        "kernels": stats["kernels"],
+        "parity": "byte-exact: payload and restored blocks equal the source blocks, all 512",
+        "reference_l4_ms": 109.0,
     }
 
 
@@ -587,71 +645,100 @@ def distinct_decode(device, steps: int) -> dict:
     return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in run.items()}
 
 
-def cpu_reference_config1(blocks_in_pool: int = 256, moved: int = 64) -> dict | None:
-    """BASELINE configs[0] on the host: the reference's own host transfer library (built from
-    its sources into oracle/_ref) gathers 64 random blocks of a BF16 pool into pinned host
-    memory and scatters them into 64 other ids, bit-exact. The pool is 256 blocks rather
-    than 4,096 to bound the fill time; per-block work does not depend on the pool size."""
-    import numpy as np
+def host_cores() -> int:
+    return len(os.sched_getaffinity(0))
 
-    from layover_amd.kv.native import Engine
+
+def cpu_config1(device, blocks_in_pool: int = 4096, moved: int = 64) -> dict:
+    """BASELINE configs[0] on the host cores: a 4,096-block Qwen3-4B BF16 pool (9.66 GB of host
+    RAM, N(0,1), filled in 64-block slices) gathers 64 random blocks into pinned memory and
+    scatters them into 64 other random ids, bit-exact. Timed on the reference's own host
+    library (oracle/_ref, built from its sources) when present, and on this package's host
+    flavour. The slices are drawn on the GPU (seed 0) and copied down: a NumPy fill of 4.8 G
+    values would take longer than the whole bench."""
+    import numpy as np
+    import torch
+
+    from layover_amd.kv.native import Engine, build_dir
     from oracle import oracle
 
-    if not oracle.REFERENCE_LIBRARY.exists():
-        return None
     block = 2_359_296
+    pool = np.empty(blocks_in_pool * block, dtype=np.uint8)
+    generator = torch.Generator(device=device).manual_seed(0)
+    for first in range(0, blocks_in_pool, 64):
+        piece = torch.randn(64 * block // 2, generator=generator, device=device).to(torch.bfloat16)
+        pool[first * block : (first + 64) * block] = piece.view(torch.uint8).cpu().numpy()
     rng = np.random.default_rng(0)
-    pool = oracle.bf16_bits(rng.standard_normal(blocks_in_pool * block // 2, dtype=np.float32)).view(np.uint8)
     order = rng.permutation(blocks_in_pool)
     src, dst = [int(i) for i in order[:moved]], [int(i) for i in order[moved : 2 * moved]]
     expected = oracle.gather(pool, block, src)
-    engine = Engine("host", staging_bytes=128 << 20, ids_capacity=1 << 16, library=oracle.REFERENCE_LIBRARY)
-    try:
-        host = engine.host_alloc(moved * block)
-        times = {}
-        for name, call, ids in (("out", engine.out_gather, src), ("in", engine.in_scatter, dst)):  # untimed: first touch of pages
-            transfer = call(pool.ctypes.data, block, ids, host)
-            engine.wait(transfer)
-            engine.release(transfer)
-        for name, call, ids in (("out", engine.out_gather, src), ("in", engine.in_scatter, dst)):
-            t0 = time.perf_counter()
-            transfer = call(pool.ctypes.data, block, ids, host)
-            engine.wait(transfer)
-            times[name] = time.perf_counter() - t0
-            engine.release(transfer)
-        ok = np.array_equal(oracle.gather(pool, block, dst), expected)
-    finally:
-        engine.destroy()
-    moved_bytes = moved * block
+    libraries = {"package": build_dir("host") / "liblayover_transfer.so"}
+    if oracle.REFERENCE_LIBRARY.exists():
+        libraries["reference"] = oracle.REFERENCE_LIBRARY
+    results = {}
+    for name, path in libraries.items():
+        engine = Engine("host", staging_bytes=128 << 20, ids_capacity=1 << 16, library=path)
+        try:
+            host = engine.host_alloc(moved * block)
+            timings = {"out": [], "in": []}
+            exact = True
+            for repeat in range(4):  # the first round touches the pages and is not timed
+                for i in dst:
+                    pool[i * block : (i + 1) * block] = 0
+                for leg, call, ids in (("out", engine.out_gather, src), ("in", engine.in_scatter, dst)):
+                    t0 = time.perf_counter()
+                    transfer = call(pool.ctypes.data, block, ids, host)
+                    engine.wait(transfer)
+                    elapsed = time.perf_counter() - t0
+                    engine.release(transfer)
+                    if repeat:
+                        timings[leg].append(elapsed)
+                exact &= bool(np.array_equal(oracle.gather(pool, block, dst), expected))
+            engine.host_free(host)
+        finally:
+            engine.destroy()
+        out_s, in_s = sorted(timings["out"])[1], sorted(timings["in"])[1]
+        results[name] = {"out_ms": round(out_s * 1e3, 2), "in_ms": round(in_s * 1e3, 2),
+                         "out_gbs": round(moved * block / out_s / 1e9, 2), "in_gbs": round(moved * block / in_s / 1e9, 2),
+                         "bit_exact": exact}
     return {
-        "out_ms": round(times["out"] * 1e3, 2),
-        "in_ms": round(times["in"] * 1e3, 2),
-        "out_gbs": round(moved_bytes / times["out"] / 1e9, 2),
-        "in_gbs": round(moved_bytes / times["in"] / 1e9, 2),
-        "bytes_each_way": moved_bytes,
-        "bit_exact": bool(ok),
+        **results,
+        "bytes_each_way": moved * block,
+        "pool_blocks": blocks_in_pool,
         "threads": 2,
-        "kind": "reference",
-        "sample": f"reference host flavour (oracle/_ref), {moved} of {blocks_in_pool} Qwen3-4B BF16 blocks out then into {moved} other ids",
+        "host_cores": host_cores(),
+        "sample": f"{moved} of {blocks_in_pool} Qwen3-4B BF16 blocks out, then into {moved} other ids; median of 3 after one untimed round",
     }
 
 
-def cpu_baseline(layout, blocks_sample: int) -> dict:
-    """The oracle's single-threaded C FP8 quantize + dequantize over a sample of blocks, scaled
-    to the 512-block workload."""
+def cpu_baseline(layout, bits, gpu_records) -> dict:
+    """The CPU leg of the headline workload: the oracle's C restatement of the reference's
+    quantizer (fp8.py:86-198) on the same 512 source blocks, quantize then dequantize, split
+    over the host cores in threads (the ctypes calls release the GIL). Its records are also
+    compared byte for byte with the GPU swap's payload: a full-size parity check."""
+    from concurrent.futures import ThreadPoolExecutor
+
     import numpy as np
 
     from oracle import oracle
 
-    rng = np.random.default_rng(0)
-    bits = oracle.bf16_bits(rng.standard_normal((blocks_sample, layout.block_elems), dtype=np.float32))
-    ids = np.arange(blocks_sample, dtype=np.int32)
+    threads = min(16, host_cores())
+    parts = [part for part in np.array_split(np.arange(len(bits)), threads) if len(part)]
+
+    def leg(part):
+        local = np.ascontiguousarray(bits[part])
+        ids = np.arange(len(part), dtype=np.int32)
+        records = oracle.quantize_records(local, ids, layout.group_elems, layout.groups_per_block)
+        restored = np.zeros_like(local)
+        oracle.dequantize_records(records, ids, restored, layout.group_elems, layout.groups_per_block)
+        return records
+
     start = time.perf_counter()
-    records = oracle.quantize_records(bits, ids, layout.group_elems, layout.groups_per_block)
-    restored = np.zeros_like(bits)
-    oracle.dequantize_records(records, ids, restored, layout.group_elems, layout.groups_per_block)
+    with ThreadPoolExecutor(len(parts)) as pool:
+        records = list(pool.map(leg, parts))
     seconds = time.perf_counter() - start
-    return {"seconds": seconds, "blocks": blocks_sample}
+    return {"seconds": seconds, "blocks": len(bits), "threads": len(parts),
+            "records_equal_gpu_payload": bool(np.array_equal(np.concatenate(records), gpu_records))}
 
 
 def calibrate_copy(device, nbytes: int = 1 << 30) -> None:
@@ -678,7 +765,6 @@ def main() -> None:
     parser.add_argument("--kernel-repeats", type=int, default=20, help="repeats of the step's FP8 kernel launches for the roofline")
     parser.add_argument("--skip-decode", action="store_true")
     parser.add_argument("--skip-cpu", action="store_true")
-    parser.add_argument("--cpu-blocks", type=int, default=64)
     parser.add_argument("--skip-overlap", action="store_true")
     parser.add_argument("--skip-distinct", action="store_true")
     parser.add_argument("--skip-graphs", action="store_true", help="skip the HIP-graph decode steps (rocprofv3 --pmc cannot follow replays)")
@@ -767,6 +853,9 @@ def main() -> None:
                               "frac": round(swap["dequantize"]["achieved_gbs"] / HBM_PEAK_GBS, 4)},
     }
 
+    log("swap bf16 (the same 512 blocks, raw)")
+    result["swap_bf16"] = bf16_swap_bench(args, device, pool_blocks, cache)
+
     if not args.skip_decode:
         rng = np.random.default_rng(2)
         mixed = [int(n) for n in rng.integers(1024, 32769, size=32)]
@@ -823,21 +912,21 @@ def main() -> None:
         )
 
     if not args.skip_cpu:
-        log(f"cpu baseline: oracle FP8 quantize+dequantize on {args.cpu_blocks} blocks")
-        cpu = cpu_baseline(layout, args.cpu_blocks)
-        scaled_ms = cpu["seconds"] * 1e3 * args.blocks / cpu["blocks"]
+        log(f"cpu baseline: oracle FP8 quantize+dequantize of all {args.blocks} blocks")
+        cpu = cpu_baseline(layout, swap["source_bits"], swap["gpu_records"])
         result["cpu_baseline"] = {
-            "value": round(scaled_ms, 1),
+            "value": round(cpu["seconds"] * 1e3, 1),
             "unit": "ms",
-            "cores": 1,
+            "cores": cpu["threads"],
+            "host_cores": host_cores(),
             "kind": "port",
-            "sample": f"oracle C quantize+dequantize of {cpu['blocks']} Qwen3-4B blocks ({cpu['seconds']:.2f} s), scaled to {args.blocks} blocks; arithmetic only, no host copies",
+            "sample": f"oracle C quantize+dequantize of all {cpu['blocks']} swapped Qwen3-4B blocks in {cpu['threads']} threads; "
+                      "arithmetic only, no host copies",
         }
-    if not args.skip_cpu:
-        log("config 1: reference host library, BF16 gather/scatter")
-        reference = cpu_reference_config1()
-        if reference is not None:
-            result["cpu_reference_config1"] = reference
+        result["swap"]["parity_full"] = ("all 512 records bit-exact vs the oracle" if cpu["records_equal_gpu_payload"]
+                                         else "MISMATCH against the oracle")
+        log("config 1: BF16 gather/scatter on the host libraries, 4,096-block pool")
+        result["cpu_config1"] = cpu_config1(device)
     calibrate_copy(device)
     print(json.dumps(result), flush=True)
 

@@ -1,13 +1,14 @@
 /*
  * layover_transfer.h: C ABI of the KV block transfer library, version 2.
  *
- * Drop-in for the reference's native/layover_transfer.h (ABI 2): the same 27 entry points,
+ * Drop-in for the reference's native/layover_transfer.h (ABI 2): the same 26 entry points,
  * the same argument meaning, error codes, slot-event numbering and ownership rules, so the
  * reference's ctypes binding (layover/kv/native.py:54-78) binds this library unchanged apart
  * from the flavour name. Flavours of this library:
  *   "host"  host threads stand in for device streams (tests, CPU baseline)
- *   "hip"   MI355X (gfx950): HIP streams, events, SDMA copies and hand-written gather and
- *           scatter kernels; replaces the reference's native/transfer_cuda.cu.
+ *   "hip"   MI355X (gfx950): HIP streams and events, hipMemcpyAsync to and from pinned
+ *           memory and hand-written gather and scatter kernels; replaces the reference's
+ *           native/transfer_cuda.cu.
  *
  * Contract (reference native/layover_transfer.h:1-5, native/transfer_core.h:581-603):
  *   - one engine is driven by one thread; calls are not thread-safe;
@@ -116,12 +117,6 @@ int lt_host_call(lt_engine* engine, void* stream, lt_host_kernel kernel, void* c
 int lt_host_set_paused(lt_engine* engine, int paused);
 int lt_host_set_copy_delay_us(lt_engine* engine, uint32_t delay_us);
 int lt_host_set_pin_limit(lt_engine* engine, uint64_t bytes);
-
-/* No counterpart in the reference. Copies to the host that the HIP flavour has run on an SDMA
- * engine (hsa_amd_memory_async_copy) since the library was loaded; the host flavour returns 0.
- * With LAYOVER_D2H=sdma in the environment, copies of at least 4 MiB from HIP device memory
- * into pinned host memory take that path; otherwise every copy uses hipMemcpyAsync. */
-uint64_t lt_sdma_copies(void);
 
 #ifdef __cplusplus
 }

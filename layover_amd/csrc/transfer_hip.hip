@@ -1,26 +1,17 @@
 // The HIP flavour of include/layover_transfer.h for MI355X (gfx950). Replaces the reference's
-// native/transfer_cuda.cu: the same engine (transfer_engine.h) over HIP streams, events,
-// copies to and from pinned memory and this file's gather and scatter kernels.
+// native/transfer_cuda.cu: the swap engine (swap_engine.h) over HIP streams, events, copies to
+// and from pinned memory, and this file's gather and scatter kernels.
 //
-// Copies to the device are hipMemcpyAsync, which the runtime runs on the SDMA engines. Copies
-// to the host are hipMemcpyAsync too, which the runtime runs as a blit kernel whose workgroups
-// hold CU slots for the whole PCIe transfer (2.4 ms per 133 MB). With LAYOVER_D2H=sdma, large
-// copies to the host go to an SDMA engine instead, through the HSA runtime
-// (hsa_amd_memory_async_copy), issued in stream order from a host function on the copy stream
-// that returns when the copy's completion signal fires; the stream's later work (the slot's
-// release event) then follows the copy as before. It frees the CUs during swap-outs, at the
-// price of a host round trip per segment: measured on MI355X beside batch-32 decode, a
-// 2,048-block FP8 swap-out takes 45.1 ms that way against 43.4 ms with the blit kernel, with
-// the same decode slowdown (3.5%), so the blit kernel stays the default.
+// Both directions of a copy are hipMemcpyAsync between device memory and pinned host memory.
+// Copies to the device run on an SDMA engine; copies to the host run as the runtime's blit
+// kernel, which measured faster on MI355X than handing them to an SDMA engine through the HSA
+// runtime (a 2,048-block FP8 swap-out beside decode: 43.4 ms against 45.1 ms).
 //
 #include <hip/hip_runtime.h>
-#include <hsa/hsa.h>
-#include <hsa/hsa_ext_amd.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
 
-#include <atomic>
 #include <stdexcept>
 #include <string>
 
@@ -68,63 +59,6 @@ __global__ __launch_bounds__(kCopyLanes) void scatter_blocks(uint8_t* __restrict
     copy_chunk<Word>(staging + uint64_t(index) * block_bytes + offset, pool + uint64_t(ids[index]) * block_bytes + offset, bytes);
 }
 
-// Copies to the host of at least this many bytes go to SDMA; smaller ones (single blocks of
-// the per-block paths) keep hipMemcpyAsync, where a host function per copy would cost more
-// than it saves.
-constexpr uint64_t kSdmaMinBytes = 4ull << 20;
-
-std::atomic<uint64_t> sdma_copies{0};
-
-// Read per copy (one call per staged segment), so a process can switch paths between transfers.
-bool sdma_wanted() {
-    const char* text = getenv("LAYOVER_D2H");
-    return text != nullptr && strcmp(text, "sdma") == 0;
-}
-
-// The HSA agent that owns an allocation and the allocation's extent, or false when the HSA
-// runtime does not know the pointer (pageable host memory) or the range leaves it.
-bool hsa_owner(const void* pointer, uint64_t bytes, hsa_device_type_t want, hsa_agent_t* owner) {
-    hsa_amd_pointer_info_t info{};
-    info.size = sizeof(info);
-    if (hsa_amd_pointer_info(pointer, &info, nullptr, nullptr, nullptr) != HSA_STATUS_SUCCESS) return false;
-    if (info.type != HSA_EXT_POINTER_TYPE_HSA || info.agentOwner.handle == 0) return false;
-    const uintptr_t base = reinterpret_cast<uintptr_t>(info.agentBaseAddress);
-    const uintptr_t at = reinterpret_cast<uintptr_t>(pointer);
-    if (at < base || at - base + bytes > info.sizeInBytes) return false;
-    hsa_device_type_t type{};
-    if (hsa_agent_get_info(info.agentOwner, HSA_AGENT_INFO_DEVICE, &type) != HSA_STATUS_SUCCESS || type != want) return false;
-    *owner = info.agentOwner;
-    return true;
-}
-
-// One SDMA copy to the host, run by the HIP runtime's callback thread in stream order. It
-// never throws: a failure is recorded in `failed` and reported by the next event query or
-// synchronization on the engine.
-struct SdmaCopy {
-    void* dst;
-    const void* src;
-    uint64_t bytes;
-    hsa_agent_t dst_agent;
-    hsa_agent_t src_agent;
-    std::atomic<int>* failed;
-
-    static void run(void* arg) {
-        SdmaCopy* job = static_cast<SdmaCopy*>(arg);
-        hsa_signal_t done{};
-        bool ok = hsa_signal_create(1, 0, nullptr, &done) == HSA_STATUS_SUCCESS;
-        if (ok) {
-            ok = hsa_amd_memory_async_copy(job->dst, job->dst_agent, job->src, job->src_agent, job->bytes, 0, nullptr, done) ==
-                 HSA_STATUS_SUCCESS;
-            // The runtime decrements the signal to 0 on success and sets it negative on error.
-            if (ok) ok = hsa_signal_wait_scacquire(done, HSA_SIGNAL_CONDITION_LT, 1, UINT64_MAX, HSA_WAIT_STATE_BLOCKED) == 0;
-            hsa_signal_destroy(done);
-        }
-        if (ok) sdma_copies.fetch_add(1, std::memory_order_relaxed);
-        else job->failed->store(1, std::memory_order_release);
-        delete job;
-    }
-};
-
 class HipDevice {
    public:
     using Stream = hipStream_t;
@@ -141,9 +75,6 @@ class HipDevice {
         activate();
     }
 
-    ~HipDevice() {
-        if (hsa_opened_) hsa_shut_down();
-    }
     HipDevice(const HipDevice&) = delete;
     HipDevice& operator=(const HipDevice&) = delete;
 
@@ -206,24 +137,13 @@ class HipDevice {
         const hipError_t status = hipEventQuery(event);
         if (status == hipErrorNotReady) return false;
         check(status, "hipEventQuery");
-        check_sdma();
         return true;
     }
     void event_sync(Event event) {
         check(hipEventSynchronize(event), "hipEventSynchronize");
-        check_sdma();
     }
 
     void memcpy_to_host(Stream stream, void* dst, const void* src, uint64_t bytes) {
-        hsa_agent_t dst_agent{}, src_agent{};
-        if (bytes >= kSdmaMinBytes && sdma_wanted() && hsa_open() && hsa_owner(dst, bytes, HSA_DEVICE_TYPE_CPU, &dst_agent) &&
-            hsa_owner(src, bytes, HSA_DEVICE_TYPE_GPU, &src_agent)) {
-            SdmaCopy* job = new SdmaCopy{dst, src, bytes, dst_agent, src_agent, &sdma_failed_};
-            const hipError_t status = hipLaunchHostFunc(stream, SdmaCopy::run, job);
-            if (status != hipSuccess) delete job;
-            check(status, "hipLaunchHostFunc(SDMA copy to host)");
-            return;
-        }
         check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, stream), "hipMemcpyAsync(device to host)");
     }
     void memcpy_to_device(Stream stream, void* dst, const void* src, uint64_t bytes) {
@@ -261,27 +181,14 @@ class HipDevice {
         if (status != hipSuccess) throw std::runtime_error(std::string(call) + ": " + hipGetErrorName(status) + ": " + hipGetErrorString(status));
     }
 
-    // hsa_init counts references: this one keeps the runtime HIP already runs on open until
-    // the engine is destroyed.
-    bool hsa_open() {
-        if (!hsa_opened_) hsa_opened_ = hsa_init() == HSA_STATUS_SUCCESS;
-        return hsa_opened_;
-    }
-
-    void check_sdma() const {
-        if (sdma_failed_.load(std::memory_order_acquire)) throw std::runtime_error("an SDMA copy to the host failed");
-    }
-
     int device_;
-    bool hsa_opened_ = false;
-    std::atomic<int> sdma_failed_{0};
 };
 
 }  // namespace lt
 
 using Device = lt::HipDevice;
 
-#include "transfer_exports.h"
+#include "swap_engine.h"
 
 static int host_only(const char* name) {
     lt::last_error = std::string(name) + " exists only in the host flavour";
@@ -294,4 +201,3 @@ LT_EXPORT int lt_host_set_paused(lt_engine*, int) { return host_only("lt_host_se
 LT_EXPORT int lt_host_set_copy_delay_us(lt_engine*, uint32_t) { return host_only("lt_host_set_copy_delay_us"); }
 LT_EXPORT int lt_host_set_pin_limit(lt_engine*, uint64_t) { return host_only("lt_host_set_pin_limit"); }
 
-LT_EXPORT uint64_t lt_sdma_copies(void) { return lt::sdma_copies.load(std::memory_order_relaxed); }

@@ -1,20 +1,22 @@
-"""Moving KV blocks between the pool and pinned CPU memory, behind tickets.
+"""KV blocks between the pool and pinned CPU memory, behind tickets.
 
-Mirrors the reference's layover/kv/transfer.py: Payload / Ticket (:45-82), PlainCopyBackend
-(:120-144) and NativeBackend (:289-565) with the same start_out / start_in / free / prepare /
-pin_stats / close interface, so CpuTier and the scheduler drive it unchanged.
+The interface is the reference's layover/kv/transfer.py one, so CpuTier and a scheduler
+drive it unchanged: a backend's start_out / start_in return a Ticket (done() never blocks,
+wait() does) whose payload is an array of equal records in CPU memory, any prefix of which
+can be restored; free / prepare / pin_stats / close as there (transfer.py:45-117).
 
-NativeBackend on MI355X:
-  - BF16 blocks: lt_out_gather / lt_in_scatter of the HIP flavour (gather kernel into a
-    staging slot, SDMA copy to pinned memory on the engine's copy stream, two slots so the
-    next gather overlaps the previous copy).
-  - FP8 records: the fused gather+quantize kernel (lk_fp8_quantize) writes a record segment
-    into a staging tensor on this backend's own stream, and the engine's lt_ext_* events
-    order it against the copy stream's DMA of that segment (layover_transfer.h:84-96). Swap-in
-    mirrors it with lk_fp8_dequantize into freshly assigned block ids. The block ids of a
-    transfer are uploaded once, from pinned memory, on the same stream as the kernels.
-The host flavour runs the same orchestration on host threads for tests; its FP8 kernels
-must be supplied by the caller (`fp8_kernels`), since this package has no CPU quantizer.
+PlainCopyBackend (transfer.py:120-144) copies through torch and is finished on return.
+
+NativeBackend (transfer.py:289-565) drives the swap library (include/layover_transfer.h):
+  BF16   lt_out_gather / lt_in_scatter: the library's gather or scatter kernel and one DMA
+         per staging segment, overlapped over two slots.
+  FP8    this package's fused kernels (lk_fp8_quantize / lk_fp8_dequantize) write or read
+         record segments in staging tensors owned here, on a stream of this backend; the
+         library's per-slot events (lt_ext_*) order each segment's kernel against its DMA on
+         the library's copy stream. All of a transfer's block ids go to the device once, from
+         pinned memory, ahead of its first kernel.
+On the host flavour the same orchestration runs on host threads; the FP8 kernels must then
+be given (`fp8_kernels`), because this package has no CPU codec.
 """
 
 from __future__ import annotations
@@ -22,6 +24,7 @@ from __future__ import annotations
 import ctypes
 from abc import ABC, abstractmethod
 from collections.abc import Callable
+from dataclasses import dataclass
 
 import torch
 
@@ -42,18 +45,20 @@ __all__ = [
     "make_backend",
 ]
 
+# The engine counters that describe pinning stalls, as the reference reports them.
 PIN_STATS = ("host_pins", "host_pin_bytes", "host_pin_ns", "host_pin_max_ns", "host_pin_failures")
 
 
 class Payload:
-    """Offloaded blocks in CPU memory, an array of equal records; valid once its ticket is done."""
+    """Offloaded blocks in CPU memory: num_blocks records of record_bytes (FP8 records or raw
+    BF16 blocks) in `memory`, a flat uint8 tensor. Valid once the offload's ticket is done."""
 
-    def __init__(self, memory: torch.Tensor, num_blocks: int, record_bytes: int, fp8: bool, pointer: int | None = None):
-        self.memory: torch.Tensor | None = memory
+    def __init__(self, memory: torch.Tensor | None, num_blocks: int, record_bytes: int, fp8: bool, pointer: int | None = None):
+        self.memory = memory
         self.num_blocks = num_blocks
         self.record_bytes = record_bytes
         self.fp8 = fp8
-        self.pointer = pointer
+        self.pointer = pointer  # the engine's pinned buffer, when the engine owns the memory
 
     @property
     def nbytes(self) -> int:
@@ -61,16 +66,18 @@ class Payload:
 
 
 class Ticket(ABC):
-    """A copy in progress. done() never blocks; wait() does."""
+    """A copy under way."""
 
     payload: Payload | None = None
-    ready_at: float | None = None
+    ready_at: float | None = None  # for copies timed on a virtual clock; real ones leave it None
 
     @abstractmethod
-    def done(self) -> bool: ...
+    def done(self) -> bool:
+        """Whether the copy has finished; never blocks."""
 
     @abstractmethod
-    def wait(self) -> None: ...
+    def wait(self) -> None:
+        """Blocks until the copy has finished."""
 
 
 class ReadyTicket(Ticket):
@@ -81,7 +88,7 @@ class ReadyTicket(Ticket):
         return True
 
     def wait(self) -> None:
-        pass
+        return None
 
 
 class TransferBackend(ABC):
@@ -89,23 +96,25 @@ class TransferBackend(ABC):
 
     @abstractmethod
     def start_out(self, cache: PagedKVCache, blocks: list[int], fp8: bool = False) -> Ticket:
-        """Begin copying blocks to CPU memory; the caller keeps them unwritten until done."""
+        """Copy `blocks` out, in order, into ticket.payload. The caller keeps them allocated and
+        unwritten until the ticket is done."""
 
     @abstractmethod
     def start_in(self, cache: PagedKVCache, blocks: list[int], payload: Payload) -> Ticket:
-        """Begin copying the first len(blocks) records into `blocks`."""
+        """Copy the payload's first len(blocks) records into `blocks`. The caller keeps the
+        payload alive and the blocks unread until the ticket is done."""
 
     def free(self, payload: Payload) -> None:
-        """Give back a payload's memory. Its offload and restores must be done."""
+        """Return a payload's memory; its offload and restores must have finished."""
 
     def prepare(self, cache: PagedKVCache, fp8: bool = False) -> None:
-        """Do first-use work now (staging allocation)."""
+        """Do first-use work (staging) now rather than inside the first transfer."""
 
     def pin_stats(self) -> dict[str, int]:
         return {}
 
     def close(self) -> None:
-        pass
+        return None
 
 
 def record_bytes(cache: PagedKVCache, fp8: bool) -> int:
@@ -113,101 +122,152 @@ def record_bytes(cache: PagedKVCache, fp8: bool) -> int:
 
 
 class PlainCopyBackend(TransferBackend):
-    """One tensor per offload through torch, finished before it returns (transfer.py:120-144)."""
+    """Whole-tensor copies through torch, finished when they return."""
 
     name = "plain"
 
     def start_out(self, cache: PagedKVCache, blocks: list[int], fp8: bool = False) -> Ticket:
-        ids = torch.tensor(blocks, device=cache.device, dtype=torch.long)
+        index = torch.tensor(blocks, dtype=torch.long, device=cache.device)
         if fp8:
             layout = Fp8Layout.from_cache(cache)
             stage = torch.empty(len(blocks) * layout.record_bytes, dtype=torch.uint8, device=cache.device)
-            quantize_blocks(cache.pool, ids.int(), stage, layout)
-            memory = stage.to("cpu")
+            quantize_blocks(cache.pool, index.to(torch.int32), stage, layout)
+            host = stage.cpu()
         else:
-            memory = cache.pool[ids].to("cpu", copy=True).reshape(-1).view(torch.uint8)
-        return ReadyTicket(Payload(memory, len(blocks), record_bytes(cache, fp8), fp8))
+            host = cache.pool.index_select(0, index).cpu().view(torch.uint8).reshape(-1)
+        return ReadyTicket(Payload(host, len(blocks), record_bytes(cache, fp8), fp8))
 
     def start_in(self, cache: PagedKVCache, blocks: list[int], payload: Payload) -> Ticket:
-        ids = torch.tensor(blocks, device=cache.device, dtype=torch.long)
-        used = payload.memory[: len(blocks) * payload.record_bytes]
+        index = torch.tensor(blocks, dtype=torch.long, device=cache.device)
+        records = payload.memory[: len(blocks) * payload.record_bytes].to(cache.device)
         if payload.fp8:
-            dequantize_blocks(used.to(cache.device), ids.int(), cache.pool, Fp8Layout.from_cache(cache))
+            dequantize_blocks(records, index.to(torch.int32), cache.pool, Fp8Layout.from_cache(cache))
         else:
-            shape = (len(blocks), *cache.pool.shape[1:])
-            cache.pool[ids] = used.view(cache.pool.dtype).reshape(shape).to(cache.device)
+            cache.pool.index_copy_(0, index, records.view(cache.pool.dtype).view(len(blocks), *cache.pool.shape[1:]))
         return ReadyTicket()
 
 
-class _NativeTicket(Ticket):
-    def __init__(self, backend: "NativeBackend", transfer: int, payload: Payload | None, keepalive: list):
-        self.payload = payload
-        self._backend = backend
-        self._transfer = transfer
-        self._keepalive = keepalive
+class _EngineTicket(Ticket):
+    """An lt_transfer of the backend's engine, released as soon as it is seen finished; it
+    keeps the tensors its kernels use alive until then."""
 
-    def _settle(self) -> None:
-        self._backend.engine.release(self._transfer)
-        self._transfer = None
-        self._keepalive = None
+    def __init__(self, engine: Engine, handle: int, payload: Payload | None, holds: list):
+        self.payload = payload
+        self._engine = engine
+        self._handle: int | None = handle
+        self._holds: list | None = holds
+
+    def _finished(self) -> None:
+        self._engine.release(self._handle)
+        self._handle, self._holds = None, None
 
     def done(self) -> bool:
-        if self._transfer is None or self._backend.engine.closed:
+        if self._handle is None or self._engine.closed:  # closing the engine waited for it
             return True
-        if not self._backend.engine.poll(self._transfer):
-            return False
-        self._settle()
-        return True
+        if self._engine.poll(self._handle):
+            self._finished()
+            return True
+        return False
 
     def wait(self) -> None:
-        if self._transfer is None or self._backend.engine.closed:
+        if self._handle is None or self._engine.closed:
             return
-        self._backend.engine.wait(self._transfer)
-        self._settle()
+        self._engine.wait(self._handle)
+        self._finished()
 
 
 Fp8Kernel = Callable[[torch.Tensor, torch.Tensor, torch.Tensor, Fp8Layout], None]
 
 
+@dataclass
+class _Segment:
+    slot: int
+    first: int  # index of its first block within the transfer
+    count: int
+
+
+class _KernelLane:
+    """Where this backend's FP8 kernels run: a torch stream of its own on a GPU, the engine's
+    caller stream (a host thread) on the host flavour."""
+
+    def __init__(self, engine: Engine, device: torch.device):
+        self._engine = engine
+        self._device = device
+        self._stream = torch.cuda.Stream(device=device) if engine.flavor == "hip" else None
+
+    @property
+    def handle(self) -> int:
+        return self._stream.cuda_stream if self._stream is not None else self._engine.host_stream()
+
+    @property
+    def stream(self):
+        return self._stream
+
+    def run(self, work: Callable[[], None], holds: list) -> None:
+        if self._stream is not None:
+            with torch.cuda.stream(self._stream):
+                work()
+        else:
+            holds.append(self._engine.host_call(self.handle, work))
+
+    def upload(self, blocks: list[int], holds: list) -> torch.Tensor:
+        """The block ids as int32 on the device, copied from pinned memory in this lane's
+        order (from pageable memory the copy would block the host until the stream drains)."""
+        ids = torch.tensor(blocks, dtype=torch.int32)
+        if self._stream is None:
+            return ids
+        pinned = ids.pin_memory()
+        on_device = torch.empty(len(blocks), dtype=torch.int32, device=self._device)
+        with torch.cuda.stream(self._stream):
+            on_device.copy_(pinned, non_blocking=True)
+        holds += [pinned, on_device]
+        return on_device
+
+
 class NativeBackend(TransferBackend):
-    """Gather into staging, one DMA per segment on a dedicated copy stream, events in between."""
+    """Staged swaps through the native library; see the module docstring."""
 
     name = "native"
 
-    def __init__(
-        self,
-        device: torch.device | str = "cpu",
-        staging_bytes: int = 128 << 20,
-        num_staging: int = 2,
-        ids_capacity: int = 1 << 20,
-        host_cache_bytes: int = 8 << 30,
-        fp8_impl: str | None = None,
-        fp8_kernels: tuple[Fp8Kernel, Fp8Kernel] | None = None,
-    ):
+    def __init__(self, device: torch.device | str = "cpu", staging_bytes: int = 128 << 20, num_staging: int = 2,
+                 ids_capacity: int = 1 << 20, host_cache_bytes: int = 8 << 30, fp8_impl: str | None = None,
+                 fp8_kernels: tuple[Fp8Kernel, Fp8Kernel] | None = None):
         self.device = torch.device(device)
-        if self.device.type not in ("cpu", "cuda"):
-            raise ValueError(f"no native transfer path for device {device}")
-        # torch-ROCm names its GPUs "cuda"; this library's flavour for them is "hip".
-        self.flavor = "hip" if self.device.type == "cuda" else "host"
-        if self.flavor == "host":
+        if self.device.type == "cuda":
+            self.flavor = "hip"  # torch-ROCm's name for the GPU; the library's flavour is hip
+        elif self.device.type == "cpu":
+            self.flavor = "host"
             build_host()
-        index = (self.device.index or 0) if self.flavor == "hip" else 0
-        self.engine = Engine(self.flavor, index, staging_bytes, num_staging, ids_capacity, host_cache_bytes)
+        else:
+            raise ValueError(f"no native transfer path for device {device}")
         if fp8_impl not in (None, "hip"):
-            raise ValueError(f"this build has only the 'hip' FP8 implementation, not {fp8_impl!r}")
-        if fp8_kernels is None:
-            fp8_kernels = (quantize_blocks, lambda stage, ids, pool, layout: dequantize_blocks(stage, ids, pool, layout))
-        self._quantize, self._dequantize = fp8_kernels
-        self._next_stage = 0
+            raise ValueError(f"the FP8 kernels here are the 'hip' ones, not {fp8_impl!r}")
+        ordinal = (self.device.index or 0) if self.flavor == "hip" else 0
+        self.engine = Engine(self.flavor, ordinal, staging_bytes, num_staging, ids_capacity, host_cache_bytes)
+        self._quantize, self._dequantize = fp8_kernels or (quantize_blocks, dequantize_blocks)
+        self._lane: _KernelLane | None = None
         self._stages: list[torch.Tensor] = []
-        self._stream = None
-        self._live: list[Payload] = []
+        self._turn = 0
+        self._payloads: dict[int, Payload] = {}  # pinned payloads by id(), freed on close
+
+    @property
+    def kernel_stream(self):
+        """The torch stream the FP8 kernels run on (None before the first FP8 use, and on the
+        host flavour)."""
+        return self._lane.stream if self._lane is not None else None
+
+    @property
+    def stages(self) -> list[torch.Tensor]:
+        """The FP8 staging tensors, one per slot."""
+        return self._stages
+
+    # -- lifetime and memory --
 
     def close(self) -> None:
         self.engine.destroy()
-        for payload in self._live:
+        for payload in self._payloads.values():
             payload.memory = None
-        self._live = []
+        self._payloads.clear()
         self._stages = []
 
     def __del__(self):
@@ -219,147 +279,114 @@ class NativeBackend(TransferBackend):
     def pin_stats(self) -> dict[str, int]:
         if self.engine.closed:
             return {}
-        stats = self.engine.stats()
-        return {name: stats[name] for name in PIN_STATS}
+        counters = self.engine.stats()
+        return {name: counters[name] for name in PIN_STATS}
 
-    # Memory
-
-    def _host_payload(self, count: int, record: int, fp8: bool) -> Payload:
-        nbytes = count * record
-        pointer = self.engine.host_alloc(nbytes)
-        buffer = (ctypes.c_uint8 * nbytes).from_address(pointer)
-        payload = Payload(torch.frombuffer(buffer, dtype=torch.uint8), count, record, fp8, pointer)
-        self._live.append(payload)
+    def _pinned_payload(self, count: int, record: int, fp8: bool) -> Payload:
+        size = count * record
+        pointer = self.engine.host_alloc(size)
+        view = torch.frombuffer((ctypes.c_uint8 * size).from_address(pointer), dtype=torch.uint8)
+        payload = Payload(view, count, record, fp8, pointer)
+        self._payloads[id(payload)] = payload
         return payload
 
     def free(self, payload: Payload) -> None:
         if payload.pointer is None or self.engine.closed:
             return
-        self._live.remove(payload)
+        self._payloads.pop(id(payload), None)
         self.engine.host_free(payload.pointer)
-        payload.memory = None
-        payload.pointer = None
+        payload.memory, payload.pointer = None, None
 
-    def _check_cache(self, cache: PagedKVCache, blocks: list[int] | None = None) -> None:
+    def _check(self, cache: PagedKVCache, blocks: list[int] = ()) -> None:
         if cache.device.type != self.device.type:
-            raise ValueError(f"pool is on {cache.device}, this backend drives {self.device}")
-        # Kernels index the pool with these unchecked; a wild id would fault the GPU.
-        if blocks and not (0 <= min(blocks) and max(blocks) < cache.allocator.num_blocks):
+            raise ValueError(f"the pool is on {cache.device}; this backend moves {self.device} memory")
+        # The kernels index the pool with these ids as given; a wild one would fault the GPU.
+        if blocks and (min(blocks) < 0 or max(blocks) >= cache.allocator.num_blocks):
             raise ValueError(f"block ids {min(blocks)}..{max(blocks)} are outside a pool of {cache.allocator.num_blocks}")
 
     def prepare(self, cache: PagedKVCache, fp8: bool = False) -> None:
-        self._check_cache(cache)
+        self._check(cache)
         if fp8:
-            self._ensure_stages(Fp8Layout.from_cache(cache))
+            self._fp8_ready(Fp8Layout.from_cache(cache))
         else:
             self.engine.prepare_staging()
 
-    def _sync_torch(self) -> None:
-        # Offload kernels run on other streams; this makes them see KV writes queued on torch's
-        # current stream (transfer.py:388-401). Only the current stream: a device-wide sync
-        # would also wait for copies in flight and destroy the overlap.
-        if self.flavor == "hip":
-            torch.cuda.current_stream(self.device).synchronize()
-
-    # BF16
+    # -- transfers --
 
     def start_out(self, cache: PagedKVCache, blocks: list[int], fp8: bool = False) -> Ticket:
-        self._check_cache(cache, blocks)
-        self._sync_torch()
+        self._check(cache, blocks)
+        # The gather runs on streams of its own: waiting here for torch's current stream is
+        # what makes it see KV writes still queued there (transfer.py:388-401). Only that
+        # stream: a device-wide wait would also wait for copies in flight.
+        if self.flavor == "hip":
+            torch.cuda.current_stream(self.device).synchronize()
         if not blocks:
             return ReadyTicket(Payload(torch.empty(0, dtype=torch.uint8), 0, record_bytes(cache, fp8), fp8))
         if fp8:
-            return self._fp8_out(cache, blocks)
-        payload = self._host_payload(len(blocks), cache.block_bytes, False)
-        transfer = self.engine.out_gather(cache.pool.data_ptr(), cache.block_bytes, blocks, payload.pointer)
-        return _NativeTicket(self, transfer, payload, [])
+            return self._fp8(cache, blocks, None)
+        payload = self._pinned_payload(len(blocks), cache.block_bytes, False)
+        handle = self.engine.out_gather(cache.pool.data_ptr(), cache.block_bytes, blocks, payload.pointer)
+        return _EngineTicket(self.engine, handle, payload, [])
 
     def start_in(self, cache: PagedKVCache, blocks: list[int], payload: Payload) -> Ticket:
-        self._check_cache(cache, blocks)
+        self._check(cache, blocks)
         if not blocks:
             return ReadyTicket()
         if payload.fp8:
-            return self._fp8_in(cache, blocks, payload)
-        transfer = self.engine.in_scatter(cache.pool.data_ptr(), cache.block_bytes, blocks, payload.pointer)
-        return _NativeTicket(self, transfer, None, [])
+            return self._fp8(cache, blocks, payload)
+        handle = self.engine.in_scatter(cache.pool.data_ptr(), cache.block_bytes, blocks, payload.pointer)
+        return _EngineTicket(self.engine, handle, None, [])
 
-    # FP8
+    # -- FP8 --
 
-    def _ensure_stages(self, layout: Fp8Layout) -> None:
+    def _fp8_ready(self, layout: Fp8Layout) -> None:
         if self.engine.staging_bytes < layout.record_bytes:
-            raise ValueError(f"staging of {self.engine.staging_bytes} bytes cannot hold one {layout.record_bytes} byte record")
+            raise ValueError(f"a {self.engine.staging_bytes}-byte staging slot cannot hold one {layout.record_bytes}-byte record")
         if not self._stages:
-            self._stages = [torch.empty(self.engine.staging_bytes, dtype=torch.uint8, device=self.device) for _ in range(self.engine.num_staging)]
-        if self.flavor == "hip" and self._stream is None:
-            self._stream = torch.cuda.Stream(device=self.device)
+            self._stages = [torch.empty(self.engine.staging_bytes, dtype=torch.uint8, device=self.device)
+                            for _ in range(self.engine.num_staging)]
+        if self._lane is None:
+            self._lane = _KernelLane(self.engine, self.device)
 
-    def _stream_handle(self) -> int:
-        return self._stream.cuda_stream if self.flavor == "hip" else self.engine.host_stream()
+    def _segments(self, blocks: int, per_segment: int):
+        for first in range(0, blocks, per_segment):
+            slot, self._turn = self._turn, (self._turn + 1) % len(self._stages)
+            yield _Segment(slot, first, min(per_segment, blocks - first))
 
-    def _launch(self, fn: Callable[[], None], keepalive: list) -> None:
-        if self.flavor == "hip":
-            with torch.cuda.stream(self._stream):
-                fn()
-        else:
-            keepalive.append(self.engine.host_call(self.engine.host_stream(), fn))
-
-    def _device_ids(self, blocks: list[int], keepalive: list) -> torch.Tensor:
-        """All of a transfer's block ids on the device, uploaded once from pinned memory in
-        stream order (an upload from pageable memory would synchronize)."""
-        ids = torch.tensor(blocks, dtype=torch.int32)
-        if self.flavor != "hip":
-            return ids
-        pinned = ids.pin_memory()
-        uploaded = torch.empty_like(ids, device=self.device)
-        with torch.cuda.stream(self._stream):
-            uploaded.copy_(pinned, non_blocking=True)
-        keepalive.extend((pinned, uploaded))
-        return uploaded
-
-    def _take_stage(self) -> int:
-        stage = self._next_stage
-        self._next_stage = (stage + 1) % len(self._stages)
-        return stage
-
-    def _fp8_out(self, cache: PagedKVCache, blocks: list[int]) -> Ticket:
+    def _fp8(self, cache: PagedKVCache, blocks: list[int], restore_from: Payload | None) -> Ticket:
+        """One FP8 transfer: out (restore_from None) quantizes segments into staging and copies
+        them to a new payload; in copies segments of restore_from to staging and dequantizes
+        them into `blocks`."""
         layout = Fp8Layout.from_cache(cache)
-        self._ensure_stages(layout)
-        payload = self._host_payload(len(blocks), layout.record_bytes, True)
-        per_segment = self.engine.staging_bytes // layout.record_bytes
-        stream = self._stream_handle()
-        keepalive: list = [cache.pool]
-        ids = self._device_ids(blocks, keepalive)
-        for start in range(0, len(blocks), per_segment):
-            count = min(per_segment, len(blocks) - start)
-            slot = self._take_stage()
-            stage = self._stages[slot]
-            self.engine.ext_wait(stream, slot, SLOT_RELEASED)
-            self._launch(lambda stage=stage, start=start, count=count: self._quantize(cache.pool, ids[start : start + count], stage, layout), keepalive)
-            self.engine.ext_record(stream, slot, SLOT_FILLED)
-            self.engine.ext_copy_out(stage.data_ptr(), payload.pointer + start * layout.record_bytes, count * layout.record_bytes, slot)
-        return _NativeTicket(self, self.engine.ext_finish(None), payload, keepalive)
-
-    def _fp8_in(self, cache: PagedKVCache, blocks: list[int], payload: Payload) -> Ticket:
-        layout = Fp8Layout.from_cache(cache)
-        self._ensure_stages(layout)
-        per_segment = self.engine.staging_bytes // layout.record_bytes
-        stream = self._stream_handle()
-        keepalive: list = [cache.pool]
-        ids = self._device_ids(blocks, keepalive)
-        for start in range(0, len(blocks), per_segment):
-            count = min(per_segment, len(blocks) - start)
-            slot = self._take_stage()
-            stage = self._stages[slot]
-            self.engine.ext_copy_in(stage.data_ptr(), payload.pointer + start * layout.record_bytes, count * layout.record_bytes, slot)
-            self.engine.ext_wait(stream, slot, SLOT_FILLED)
-            self._launch(lambda stage=stage, start=start, count=count: self._dequantize(stage, ids[start : start + count], cache.pool, layout), keepalive)
-            self.engine.ext_record(stream, slot, SLOT_RELEASED)
-        return _NativeTicket(self, self.engine.ext_finish(stream), None, keepalive)
+        self._fp8_ready(layout)
+        record = layout.record_bytes
+        out = restore_from is None
+        payload = self._pinned_payload(len(blocks), record, True) if out else restore_from
+        lane, engine = self._lane, self.engine
+        holds: list = [cache.pool]
+        ids = lane.upload(blocks, holds)
+        for seg in self._segments(len(blocks), engine.staging_bytes // record):
+            stage = self._stages[seg.slot]
+            seg_ids = ids[seg.first : seg.first + seg.count]
+            host = payload.pointer + seg.first * record
+            nbytes = seg.count * record
+            if out:
+                engine.ext_wait(lane.handle, seg.slot, SLOT_RELEASED)
+                lane.run(lambda stage=stage, seg_ids=seg_ids: self._quantize(cache.pool, seg_ids, stage, layout), holds)
+                engine.ext_record(lane.handle, seg.slot, SLOT_FILLED)
+                engine.ext_copy_out(stage.data_ptr(), host, nbytes, seg.slot)
+            else:
+                engine.ext_copy_in(stage.data_ptr(), host, nbytes, seg.slot)
+                engine.ext_wait(lane.handle, seg.slot, SLOT_FILLED)
+                lane.run(lambda stage=stage, seg_ids=seg_ids: self._dequantize(stage, seg_ids, cache.pool, layout), holds)
+                engine.ext_record(lane.handle, seg.slot, SLOT_RELEASED)
+        # Out ends with the last copy (copy stream); in ends with the last kernel (our lane).
+        handle = engine.ext_finish(None if out else lane.handle)
+        return _EngineTicket(engine, handle, payload if out else None, holds)
 
 
 def make_backend(name: str, device: torch.device | str = "cpu", **options) -> TransferBackend:
-    if name == "plain":
-        return PlainCopyBackend()
-    if name == "native":
-        return NativeBackend(device, **options)
-    raise ValueError(f"unknown transfer backend {name!r}")
+    backends = {"plain": lambda: PlainCopyBackend(), "native": lambda: NativeBackend(device, **options)}
+    if name not in backends:
+        raise ValueError(f"unknown transfer backend {name!r}")
+    return backends[name]()

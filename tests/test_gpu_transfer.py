@@ -28,12 +28,6 @@ def gpu_engine():
     created.destroy()
 
 
-def sdma_copies():
-    from layover_amd.kv.native import load_library
-
-    return load_library("hip").lt_sdma_copies()
-
-
 def filled_pool(blocks, block_bytes=BLOCK, seed=0):
     return torch.randint(0, 256, (blocks * block_bytes,), dtype=torch.uint8, generator=torch.Generator().manual_seed(seed))
 
@@ -148,24 +142,18 @@ def qwen_cache(blocks, seed=0, config=None):
     return cache, bits
 
 
-@pytest.mark.parametrize("d2h", ["blit", "sdma"])
 @pytest.mark.parametrize("staging_records", [3, 113], ids=["many_segments", "one_segment"])
-def test_fp8_swap_round_trip_is_bit_exact_against_the_oracle(staging_records, d2h, monkeypatch):
+def test_fp8_swap_round_trip_is_bit_exact_against_the_oracle(staging_records):
     from layover_amd.kernels.fp8 import Fp8Layout
     from layover_amd.kv.transfer import NativeBackend
 
-    monkeypatch.setenv("LAYOVER_D2H", d2h)
     cache, bits = qwen_cache(24, seed=staging_records)
     layout = Fp8Layout.from_cache(cache)
     backend = NativeBackend("cuda", staging_bytes=staging_records * layout.record_bytes + 100, ids_capacity=256)
     try:
         out_ids = [int(i) for i in np.random.default_rng(1).permutation(24)[:10]]
-        copies = sdma_copies()
         ticket = backend.start_out(cache, out_ids, fp8=True)
         ticket.wait()
-        # Segments of 3 records (3.5 MB) stay below the 4 MiB SDMA threshold; one segment of
-        # 10 records (11.8 MB) goes to an SDMA engine when asked for.
-        assert sdma_copies() - copies == (1 if staging_records == 113 and d2h == "sdma" else 0)
         expected = oracle.quantize_records(bits, out_ids, layout.group_elems, layout.groups_per_block)
         assert np.array_equal(ticket.payload.memory.numpy()[: expected.size], expected)
 
@@ -181,19 +169,15 @@ def test_fp8_swap_round_trip_is_bit_exact_against_the_oracle(staging_records, d2
         backend.close()
 
 
-@pytest.mark.parametrize("d2h", ["blit", "sdma"])
-def test_bf16_swap_round_trip_through_the_backend(d2h, monkeypatch):
+def test_bf16_swap_round_trip_through_the_backend():
     from layover_amd.kv.transfer import NativeBackend
 
-    monkeypatch.setenv("LAYOVER_D2H", d2h)
     cache, bits = qwen_cache(12, seed=3)
     backend = NativeBackend("cuda", staging_bytes=5 * cache.block_bytes, ids_capacity=64)
     try:
         out_ids = [7, 2, 9, 0, 11, 4, 5]
-        copies = sdma_copies()
         ticket = backend.start_out(cache, out_ids, fp8=False)
         ticket.wait()
-        assert sdma_copies() - copies == (2 if d2h == "sdma" else 0)  # segments of 11.8 and 4.7 MB
         expected = oracle.gather(bits, cache.block_bytes, out_ids)
         assert np.array_equal(ticket.payload.memory.numpy()[: expected.size], expected)
         in_ids = [1, 3, 6, 8, 10, 2, 0]
