@@ -431,7 +431,7 @@ def graph_decode_bench(device, cache, fp8_pool, steps: int = 20) -> list:
     for kind, pool in (("bf16", None), ("fp8", fp8_pool)):
         graphs = DecodeAttentionGraphs(cache, QWEN["query_heads"], pool=pool, sizes=(1, 8), max_tokens=32768)
         rng = np.random.default_rng(11)
-        free = [b for b in rng.permutation(cache.allocator.num_blocks).tolist() if b != graphs.scratch]
+        free = [b for b in rng.permutation(cache.allocator.num_blocks).tolist() if b not in graphs.scratch_blocks]
         for batch, tokens in ((1, 32768), (8, 4096)):
             need = -(-tokens // 16)
             tables = [BlockTable(free[i * need : (i + 1) * need], tokens) for i in range(batch)]
@@ -461,7 +461,7 @@ def graph_decode_bench(device, cache, fp8_pool, steps: int = 20) -> list:
                 "graph_kv_gbs": round(kv_bytes / (timings["graph"] * 1e-3 / QWEN["layers"]) / 1e9, 1),
                 "captured_size": size,
             })
-        cache.allocator.decref(graphs.scratch)
+        graphs.release()
         del graphs
         torch.cuda.empty_cache()
     return runs

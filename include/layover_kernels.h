@@ -172,7 +172,10 @@ int lk_fp8_append(void* records, const int32_t* write_block, const int32_t* writ
  * 139-141); for small-batch steps, which are bound by launches. The write position must be
  * the row's last token: write_block[b*write_stride] = table[b][(lengths[b] - 1) / slots] and
  * write_slot[b*write_stride] = (lengths[b] - 1) % slots, as PagedKVCache.decode_rows packs
- * them; it is not checked. Rows must name distinct blocks. Other shapes run the two launches. */
+ * them; it is not checked. Rows must name distinct blocks. On the fused path the token is
+ * written by the workgroups that read the row's last block, so a row is written only when
+ * 1 <= lengths[b] <= table_width * slots (the range lk_paged_decode accepts); a row outside it
+ * is neither read nor written. Other shapes run the two launches. */
 int lk_paged_decode_append(const lk_decode_shape* shape, const void* q, void* pool, const int32_t* table, const int32_t* lengths,
                            const int32_t* write_block, const int32_t* write_slot, uint32_t write_stride, const void* k,
                            const void* v, void* out, void* workspace, uint64_t workspace_bytes, void* stream);

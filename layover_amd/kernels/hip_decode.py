@@ -235,7 +235,8 @@ def run_kernel_append(q, pool, layer, block_table, lengths, kv_groups, write_blo
     `layer`, then run_kernel of that layer, as one decode launch where the shape allows
     (lk_paged_decode_append). The write position must be the row's last token, as the first
     two columns of PagedKVCache.decode_rows give it; that is not checked. Rows must name
-    distinct blocks. Enqueued on the current stream."""
+    distinct blocks, and a row's token is written only if 1 <= its length <= the table's
+    width x slots (decode_rows guarantees both). Enqueued on the current stream."""
     _check_layout(q, block_table, lengths, out)
     if _is_fp8(pool):
         storage, layers, kv_heads, head_dim = pool.records, pool.layers, pool.kv_heads, pool.head_dim

@@ -14,10 +14,10 @@ As in the reference, each captured batch size gets fixed input tensors: one pack
 block of rows (write block, write slot, length, block table of fixed width, as
 PagedKVCache.decode_rows builds them), q for every layer, and the new tokens' K and V. A
 batch smaller than a captured size is padded with rows of length 1 that write and read slot 0
-of a scratch block reserved here and never handed out, so a padded row cannot touch a real
-sequence's KV. Larger batches, or tables wider than the captured width, get None and run
-eagerly. The decode workspace of each size is allocated once, before capture. Padding rows all
-write the scratch block's slot 0; what it holds is never read by a real row.
+of scratch blocks reserved here and never handed out, one block per padding row (rows of a
+fused write name distinct blocks), so a padded row cannot touch a real sequence's KV. Larger
+batches, or tables wider than the captured width, get None and run eagerly. The decode
+workspace of each size is allocated once, before capture.
 """
 
 from __future__ import annotations
@@ -33,27 +33,39 @@ from layover_amd.kv.paged_cache import BlockTable, PagedKVCache
 DEFAULT_SIZES = (1, 2, 4, 8)
 
 
-def hip_graph(step: Callable[[], torch.Tensor], pool=None) -> tuple[Callable[[], None], torch.Tensor, object]:
-    """Capture `step` after running it twice on a side stream (torch's graph capture rules);
-    returns a replay function, the output tensor each replay refreshes, and the graph's memory
-    pool for the next capture to share (reference decode_graphs.py:28-40)."""
-    stream = torch.cuda.Stream()
-    stream.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(stream):
-        for _ in range(2):
-            step()
-    torch.cuda.current_stream().wait_stream(stream)
+class Replay:
+    """One captured (or eager) step: call it to run the step again; `out` is the tensor every
+    run refreshes; `memory_pool` is the graph memory pool for the next capture to share."""
+
+    def __init__(self, run: Callable[[], None], out: torch.Tensor, memory_pool):
+        self.run, self.out, self.memory_pool = run, out, memory_pool
+
+    def __call__(self) -> None:
+        self.run()
+
+
+def hip_graph(step: Callable[[], torch.Tensor], memory_pool=None) -> Replay:
+    """Records `step` as a HIP graph. torch's capture rules come first: the step runs twice on
+    a side stream that waited for the current one (so lazy allocations and library set-up
+    happen outside the capture), then the current stream waits for that warm-up."""
+    warm = torch.cuda.Stream()
+    current = torch.cuda.current_stream()
+    warm.wait_stream(current)
+    with torch.cuda.stream(warm):
+        step()
+        step()
+    current.wait_stream(warm)
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, pool=pool):
+    with torch.cuda.graph(graph, pool=memory_pool):
         out = step()
-    return graph.replay, out, graph.pool()
+    return Replay(graph.replay, out, graph.pool())
 
 
-def eager_graph(step: Callable[[], torch.Tensor], pool=None) -> tuple[Callable[[], None], torch.Tensor, object]:
-    """Runs `step` on every replay instead: the same buffers without a capture (reference
-    decode_graphs.py:43-46)."""
+def eager_graph(step: Callable[[], torch.Tensor], memory_pool=None) -> Replay:
+    """No capture: every run launches `step` again and copies its result into the same output
+    tensor, so callers see the buffers a graph would give them."""
     out = step()
-    return (lambda: out.copy_(step())), out, pool
+    return Replay(lambda: out.copy_(step()), out, memory_pool)
 
 
 class DecodeAttentionGraphs:
@@ -74,7 +86,11 @@ class DecodeAttentionGraphs:
         self.sizes = tuple(sorted(sizes))
         max_tokens = max_tokens or cache.allocator.num_blocks * cache.block_tokens
         self.width = min(cache.blocks_for(max_tokens), cache.allocator.num_blocks)
-        self.scratch = cache.allocator.alloc(1)[0]
+        # One scratch block per row of the largest size (the packed rows start as all padding):
+        # rows of a fused write must name distinct blocks, or two rows re-encoding one FP8
+        # group would race.
+        self.scratch_blocks = cache.allocator.alloc(max(self.sizes))
+        self.scratch = self.scratch_blocks[0]
         device = cache.device
         largest = self.sizes[-1]
         self.packed = torch.zeros(largest, 3 + self.width, dtype=torch.int32, device=device)
@@ -87,17 +103,20 @@ class DecodeAttentionGraphs:
         for size in self.sizes:
             shape = hip_decode.decode_shape(self.q[0, :size], self.pool, 0, self.packed[:size, 3:], self.groups)
             self._workspaces[size] = torch.empty(max(hip_decode.workspace_bytes(shape), 4), dtype=torch.uint8, device=device)
-        self._replays: dict[int, tuple[Callable[[], None], torch.Tensor]] = {}
-        graph_pool = None
+        self._replays: dict[int, Replay] = {}
+        memory_pool = None
         for size in reversed(self.sizes):  # largest first, so the smaller ones fit in its pool
-            replay, out, graph_pool = capture(lambda size=size: self._step(size), graph_pool)
-            self._replays[size] = (replay, out)
+            self._replays[size] = capture(lambda size=size: self._step(size), memory_pool)
+            memory_pool = self._replays[size].memory_pool
 
-    def _padding(self, rows: int) -> torch.Tensor:
-        """Rows of length 1 that write and read slot 0 of the scratch block."""
-        row = torch.zeros(3 + self.width, dtype=torch.int32)
-        row[0], row[1], row[2], row[3] = self.scratch, 0, 1, self.scratch
-        return row.repeat(rows, 1)
+    def _padding(self, rows: int, first: int = 0) -> torch.Tensor:
+        """`rows` rows of length 1, each writing and reading slot 0 of a scratch block of its
+        own; `first` is the index of the first padding row among a step's padding rows."""
+        padding = torch.zeros(rows, 3 + self.width, dtype=torch.int32)
+        for i in range(rows):
+            block = self.scratch_blocks[first + i]
+            padding[i, 0], padding[i, 2], padding[i, 3] = block, 1, block
+        return padding
 
     def _step(self, size: int) -> torch.Tensor:
         packed = self.packed[:size]
@@ -112,12 +131,18 @@ class DecodeAttentionGraphs:
                                          self.k_new[layer, :size], self.v_new[layer, :size], out[layer], workspace)
         return out
 
+    def release(self) -> None:
+        """Gives the scratch blocks back to the cache's allocator; the graphs are unusable after."""
+        for block in self.scratch_blocks:
+            self.cache.allocator.decref(block)
+        self.scratch_blocks = []
+
     def replay(self, size: int) -> torch.Tensor:
         """Replay the captured step of `size` rows on the buffers as they stand; returns the
         output tensor that every replay of this size refreshes."""
-        replay, out = self._replays[size]
+        replay = self._replays[size]
         replay()
-        return out
+        return replay.out
 
     def step_eager(self, size: int) -> torch.Tensor:
         """The same step launched eagerly on the same buffers, for comparison."""

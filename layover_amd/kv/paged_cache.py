@@ -10,6 +10,7 @@ from __future__ import annotations
 
 from dataclasses import dataclass, field
 
+import numpy as np
 import torch
 
 from layover_amd.config import ModelConfig
@@ -67,58 +68,71 @@ class PagedKVCache:
     def blocks_for(self, tokens: int) -> int:
         return -(-tokens // self.block_tokens)
 
-    def _to_device(self, host: torch.Tensor) -> torch.Tensor:
-        """One copy to the device, from pinned memory so it queues behind launched work
+    def _upload(self, values) -> torch.Tensor:
+        """Host values to the pool's device as one copy. On a GPU it goes through pinned memory
+        so that it is queued behind work already launched instead of waiting for it
         (paged_cache.py:103-108)."""
-        if self.device.type != "cuda":
-            return host.to(self.device)
-        return host.pin_memory().to(self.device, non_blocking=True)
+        host = torch.as_tensor(values)
+        if self.device.type == "cuda":
+            host = host.pin_memory()
+        return host.to(self.device, non_blocking=True)
 
     def chunk_locations(self, table: BlockTable, start: int, count: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-        """For tokens [start, start + count): the ids of every block they and the tokens before
-        them occupy (int32), then each token's block and slot (paged_cache.py:110-116)."""
-        if start < 0 or count < 1 or start + count > len(table.blocks) * self.block_tokens:
-            raise ValueError(f"tokens [{start}, {start + count}) do not fit a table of {len(table.blocks)} blocks")
-        ids = self._to_device(torch.tensor(table.blocks[: self.blocks_for(start + count)], dtype=torch.int32))
-        positions = torch.arange(start, start + count, device=self.device)
-        return ids, ids[positions // self.block_tokens].long(), positions % self.block_tokens
+        """Where tokens [start, start + count) of a table live (paged_cache.py:110-116): the
+        int32 ids of every block holding them or an earlier token (what a prefill chunk's
+        attention reads), then each of the tokens' block id and slot (where its K/V go)."""
+        end = start + count
+        if start < 0 or count < 1 or end > len(table.blocks) * self.block_tokens:
+            raise ValueError(f"tokens [{start}, {end}) do not fit a table of {len(table.blocks)} blocks")
+        history = self._upload(np.asarray(table.blocks[: self.blocks_for(end)], dtype=np.int32))
+        positions = torch.arange(start, end, device=self.device)
+        block_index = torch.div(positions, self.block_tokens, rounding_mode="floor")
+        return history, history.index_select(0, block_index).long(), positions - block_index * self.block_tokens
 
     def chunk(self, table: BlockTable, start: int, count: int) -> PrefillChunk:
         return PrefillChunk(start, start + count, *self.chunk_locations(table, start, count))
 
     def write_at(self, blocks: torch.Tensor, slots: torch.Tensor, layer: int, k: torch.Tensor, v: torch.Tensor) -> None:
-        """Store k and v of shape [kv_heads, count, head_dim] at the given blocks and slots
-        (paged_cache.py:118-122)."""
-        self.pool[blocks, KEY, layer, :, slots] = k.transpose(0, 1).to(self.dtype)
-        self.pool[blocks, VALUE, layer, :, slots] = v.transpose(0, 1).to(self.dtype)
+        """k and v, [kv_heads, count, head_dim], stored token by token at (blocks[t], slots[t])
+        of `layer` (paged_cache.py:118-122). The pool is addressed as rows of head_dim values:
+        row ((block * 2 + kind) * layers + layer) * kv_heads * slots + head * slots + slot."""
+        _, _, layers, kv_heads, slots_per_block, head_dim = self.pool.shape
+        rows = self.pool.view(-1, head_dim)
+        heads = torch.arange(kv_heads, device=self.device) * slots_per_block
+        for kind, values in ((KEY, k), (VALUE, v)):
+            first = ((blocks.long() * 2 + kind) * layers + layer) * kv_heads * slots_per_block + slots.long()
+            index = (first[:, None] + heads[None, :]).reshape(-1)  # [count * kv_heads], token-major
+            rows.index_copy_(0, index, values.to(self.dtype).transpose(0, 1).reshape(-1, head_dim))
 
     def read_blocks(self, ids: torch.Tensor, layer: int, end: int) -> tuple[torch.Tensor, torch.Tensor]:
-        """K and V of the first `end` tokens held in blocks `ids`, as [kv_heads, end, head_dim]
-        (paged_cache.py:124-128): the gather the paged prefill kernel avoids."""
-        ids = ids.long()
-        k = self.pool[ids, KEY, layer].permute(1, 0, 2, 3).flatten(1, 2)[:, :end]
-        v = self.pool[ids, VALUE, layer].permute(1, 0, 2, 3).flatten(1, 2)[:, :end]
-        return k, v
+        """K and V of the first `end` tokens held in blocks `ids`, each [kv_heads, end,
+        head_dim] (paged_cache.py:124-128): the gather that the paged prefill kernel avoids."""
+        picked = self.pool[:, :, layer].index_select(0, ids.long())  # [n, 2, kv_heads, slots, head_dim]
+        kv_heads, head_dim = picked.shape[2], picked.shape[4]
+        flat = picked.permute(1, 2, 0, 3, 4).reshape(2, kv_heads, -1, head_dim)[:, :, :end]
+        return flat[KEY], flat[VALUE]
 
     def decode_rows(self, tables: list[BlockTable], width: int | None = None) -> torch.Tensor:
-        """int32 [batch, 3 + width]: write block, write slot, length, then the block table padded
-        with block 0 (paged_cache.py:154-169). Checked on the host, so the decode kernel can
-        run trusted."""
+        """One packed int32 row per table (paged_cache.py:154-169): the block and slot of its
+        last token (where this step writes), its length, then its blocks, padded to `width`
+        with block 0 (a real block; nothing reads past a length). Checked here on the host,
+        so the decode kernel can run trusted."""
         width = max(len(t.blocks) for t in tables) if width is None else width
-        rows = []
-        for t in tables:
-            if not 1 <= t.num_tokens <= len(t.blocks) * self.block_tokens:
-                raise ValueError(f"a table of {len(t.blocks)} blocks cannot hold {t.num_tokens} tokens")
-            if t.blocks and not 0 <= min(t.blocks) <= max(t.blocks) < self.allocator.num_blocks:
+        rows = np.zeros((len(tables), 3 + width), dtype=np.int32)
+        for row, t in zip(rows, tables):
+            ids = np.asarray(t.blocks, dtype=np.int64)
+            if not 1 <= t.num_tokens <= ids.size * self.block_tokens:
+                raise ValueError(f"a table of {ids.size} blocks cannot hold {t.num_tokens} tokens")
+            if ids.size and (ids.min() < 0 or ids.max() >= self.allocator.num_blocks):
                 raise ValueError(f"block ids {t.blocks} are outside a pool of {self.allocator.num_blocks} blocks")
-            if len(t.blocks) > width:
-                raise ValueError(f"a table of {len(t.blocks)} blocks does not fit a width of {width}")
-            last = t.num_tokens - 1
-            rows.append([t.blocks[last // self.block_tokens], last % self.block_tokens, t.num_tokens, *t.blocks,
-                         *[0] * (width - len(t.blocks))])
-        return torch.tensor(rows, dtype=torch.int32)
+            if ids.size > width:
+                raise ValueError(f"a table of {ids.size} blocks does not fit a width of {width}")
+            where, slot = divmod(t.num_tokens - 1, self.block_tokens)
+            row[:3] = (ids[where], slot, t.num_tokens)
+            row[3 : 3 + ids.size] = ids
+        return torch.from_numpy(rows)
 
     def decode_batch(self, tables: list[BlockTable]) -> DecodeBatch:
-        rows = self.decode_rows(tables)
-        packed = rows.pin_memory().to(self.device, non_blocking=True) if self.device.type == "cuda" else rows
+        """decode_rows on the device, as the views one decode step's layers take."""
+        packed = self._upload(self.decode_rows(tables))
         return DecodeBatch(packed[:, 0].long(), packed[:, 1].long(), packed[:, 3:], packed[:, 2])

@@ -68,18 +68,23 @@ def test_append_that_raises_the_largest_exponent_requantizes_the_group():
 
 
 def stub_capture(step, pool=None):
-    return (lambda: None), None, pool
+    from layover_amd.kv.decode_graphs import Replay
+
+    return Replay(lambda: None, None, pool)
 
 
 def test_graph_bookkeeping_reserves_a_scratch_block_and_pads_with_it():
     cache = PagedKVCache(ModelConfig.micro(), 12, fill=False)
     graphs = DecodeAttentionGraphs(cache, 4, sizes=(4, 1, 2), max_tokens=100, capture=stub_capture)
     assert graphs.sizes == (1, 2, 4) and graphs.width == 7
-    assert cache.allocator.refcount(graphs.scratch) == 1
+    scratch = graphs.scratch_blocks
+    assert len(set(scratch)) == 4 and all(cache.allocator.refcount(b) == 1 for b in scratch)
     assert [graphs.size_for(n) for n in (1, 2, 3, 4, 5)] == [1, 2, 4, 4, None]
     padding = graphs._padding(2)
-    assert padding.tolist() == [[graphs.scratch, 0, 1, graphs.scratch, 0, 0, 0, 0, 0, 0]] * 2
-    assert graphs.packed.shape == (4, 10) and torch.equal(graphs.packed, padding.repeat(2, 1))
+    assert padding.tolist() == [[b, 0, 1, b, 0, 0, 0, 0, 0, 0] for b in scratch[:2]]
+    assert graphs.packed.shape == (4, 10) and torch.equal(graphs.packed, graphs._padding(4))
+    graphs.release()
+    assert cache.allocator.num_used == 0
     assert graphs.q.shape == (2, 4, 4, 24) and graphs.k_new.shape == (2, 4, 2, 24)
     assert set(graphs._workspaces) == {1, 2, 4}
 

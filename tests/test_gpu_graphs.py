@@ -186,7 +186,7 @@ def test_graph_replays_equal_the_eager_step_and_the_oracle(fp8):
         pool = fp8_pool(records, **QWEN_LIKE)
     print(f"graphs fp8={fp8}", flush=True)
     graphs = DecodeAttentionGraphs(cache, 32, pool=pool, sizes=(1, 4), max_tokens=16 * 20)
-    ids = [b for b in rng.permutation(48).tolist() if b != graphs.scratch]
+    ids = [b for b in rng.permutation(48).tolist() if b not in graphs.scratch_blocks]
     tables = [BlockTable(ids[0:20], 20 * 16), BlockTable(ids[20:21], 1), BlockTable(ids[21:24], 35)]
     q = torch.randn(36, 3, 32, 128, device="cuda").to(torch.bfloat16)
     k_new = torch.randn(36, 3, 8, 128, device="cuda").to(torch.bfloat16)
