@@ -19,7 +19,7 @@
  * Parity pins (each in tests/test_oracle.py): encode/decode against torch.float8_e4m3fn on
  * every pattern (test_fp8.py:40-59), the reference's known answers (test_fp8.py:62-153),
  * brute force of the round-trip error bound (fp8.py:25-27), record layout constants
- * (test_fp8.py:164-176), golden vectors in tests/golden/, and decode attention against
+ * (test_fp8.py:164-176), and decode attention against
  * torch's float64 scaled_dot_product_attention and a pure-Python softmax on tiny inputs.
  */
 #include <stdint.h>
