@@ -180,6 +180,16 @@ int lk_paged_decode_append(const lk_decode_shape* shape, const void* q, void* po
                            const int32_t* write_block, const int32_t* write_slot, uint32_t write_stride, const void* k,
                            const void* v, void* out, void* workspace, uint64_t workspace_bytes, void* stream);
 
+/* No counterpart in the reference. lk_paged_decode for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops that forbid hipMalloc): the same
+ * arguments minus the workspace, whose split partials go to a file-scope device array of
+ * 16 MiB per GPU (held until the process ends; its address is looked up on the first call
+ * on each device). A shape whose lk_paged_decode_workspace exceeds 16 MiB is refused with
+ * LK_ERR_INVALID. Calls on one GPU share the array: calls that overlap on one GPU race.
+ * It calls no hipMalloc or hipFree. */
+int lk_paged_decode_static(const lk_decode_shape* shape, const void* q, const void* pool, const int32_t* table,
+                           const int32_t* lengths, void* out, void* stream);
+
 /* Measurement support, no reference counterpart: stream `bytes` (a multiple of 16, 16-byte
  * aligned) from `src`, copying to `dst`, or only reading when dst is null (then `sink`, one
  * device uint32, is written only if the data hash to a value chosen never to occur). This is

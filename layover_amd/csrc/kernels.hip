@@ -6,6 +6,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
 #include <stdexcept>
 #include <string>
 
@@ -506,6 +507,52 @@ LK_EXPORT int lk_paged_decode_append(const lk_decode_shape* shape, const void* q
         lk::require(shape != nullptr, "null shape");
         const lk::TokenWrite write{write_block, write_slot, write_stride, k, v};
         lk::run_decode(*shape, q, pool, table, lengths, out, workspace, workspace_bytes, &write, static_cast<hipStream_t>(stream));
+    });
+}
+
+// lk_paged_decode_static: lk_paged_decode with its split partials in a file-scope device array
+// instead of a caller's workspace, for callers that cannot allocate. The array's address is
+// looked up once per device (hipGetSymbolAddress, with that device current) and kept; the
+// host-side name `decode_scratch` is only a stand-in and never reaches a kernel. Calls on one
+// device share the array and must not overlap; nothing in it needs clearing between calls
+// (the merge reads only the splits a row's length covers, all written by the same launch).
+namespace lk {
+
+constexpr uint64_t kStaticScratchBytes = 16ull << 20;
+constexpr int kMaxDevices = 64;
+
+static __device__ __align__(256) uint8_t decode_scratch[kStaticScratchBytes];
+
+std::mutex scratch_lock;
+void* scratch_address[kMaxDevices] = {};
+
+void* device_scratch() {
+    int device = -1;
+    require(hipGetDevice(&device) == hipSuccess && device >= 0 && device < kMaxDevices, "no usable current HIP device");
+    std::lock_guard<std::mutex> hold(scratch_lock);
+    if (scratch_address[device] == nullptr) {
+        void* address = nullptr;
+        const hipError_t status = hipGetSymbolAddress(&address, HIP_SYMBOL(decode_scratch));
+        if (status != hipSuccess || address == nullptr)
+            throw std::runtime_error(std::string("hipGetSymbolAddress(decode_scratch): ") + hipGetErrorString(status));
+        scratch_address[device] = address;
+    }
+    return scratch_address[device];
+}
+
+}  // namespace lk
+
+LK_EXPORT int lk_paged_decode_static(const lk_decode_shape* shape, const void* q, const void* pool, const int32_t* table,
+                                     const int32_t* lengths, void* out, void* stream) {
+    return lk::guarded([&] {
+        lk::require(shape != nullptr, "null shape");
+        lk::check_shape(*shape);
+        const uint64_t need = lk::workspace_bytes(*shape);
+        if (need > lk::kStaticScratchBytes)
+            throw lk::Invalid("lk_paged_decode_static: this shape needs " + std::to_string(need) + " bytes of split partials, above the " +
+                              std::to_string(lk::kStaticScratchBytes) + "-byte static scratch; use lk_paged_decode with a workspace");
+        lk::run_decode(*shape, q, pool, table, lengths, out, lk::device_scratch(), lk::kStaticScratchBytes, nullptr,
+                       static_cast<hipStream_t>(stream));
     });
 }
 
