@@ -438,9 +438,9 @@ def graph_decode_bench(device, cache, fp8_pool, steps: int = 20) -> list:
             q = torch.randn(QWEN["layers"], batch, QWEN["query_heads"], QWEN["head_dim"], device=device).to(torch.bfloat16)
             k = torch.randn(QWEN["layers"], batch, QWEN["kv_heads"], QWEN["head_dim"], device=device).to(torch.bfloat16)
             graphs.run(tables, q, k, k.clone())
-            size = graphs.size_for(batch)
+            size, width = graphs.size_for(batch), graphs.width_for(tables)
             timings = {}
-            for mode, fn in (("graph", lambda: graphs.replay(size)), ("eager", lambda: graphs.step_eager(size))):
+            for mode, fn in (("graph", lambda: graphs.replay(size, width)), ("eager", lambda: graphs.step_eager(size, width))):
                 for _ in range(3):
                     fn()
                 torch.cuda.synchronize()
@@ -460,6 +460,7 @@ def graph_decode_bench(device, cache, fp8_pool, steps: int = 20) -> list:
                 "eager_per_layer_us": round(timings["eager"] * 1e3 / QWEN["layers"], 2),
                 "graph_kv_gbs": round(kv_bytes / (timings["graph"] * 1e-3 / QWEN["layers"]) / 1e9, 1),
                 "captured_size": size,
+                "captured_width": width,
             })
         graphs.release()
         del graphs

@@ -230,8 +230,15 @@ __device__ __forceinline__ bool decode_unit_of(const DecodeArgs& a, uint32_t w, 
     return *seq < a.batch;
 }
 
-template <int KV, int QF>
-__global__ __launch_bounds__(kWave* kDecodeWaves) void decode_split_mfma(DecodeArgs a) {
+// kWaves waves per workgroup take the split's blocks round-robin: 4 for full grids; 8 when
+// the grid gives each CU at most one workgroup (small batches), so each CU has more waves
+// streaming tiles and each wave a shorter chain of dependent loads. The LDS merge keeps
+// kWaves * kHeads * kDim floats, 32 KiB either way: 8 waves hold at most 8 query heads per
+// KV head, 4 waves 16.
+template <int KV, int QF, int kWaves = kDecodeWaves>
+__global__ __launch_bounds__(kWave* kWaves) void decode_split_mfma(DecodeArgs a) {
+    constexpr uint32_t kDecodeWaves = kWaves;
+    constexpr uint32_t kHeads = kMaxHeads * 4 / kWaves;
     const uint32_t lane = threadIdx.x % kWave;
     // Wave-uniform by construction; readfirstlane tells the compiler, so values derived from
     // it stay in scalar registers.
@@ -299,39 +306,38 @@ __global__ __launch_bounds__(kWave* kDecodeWaves) void decode_split_mfma(DecodeA
     const uint64_t block_elems = uint64_t(2) * a.layers * a.kv_heads * kSlots * kDim;  // FP8: shifts follow the data
 
     // Fused decode-time write: the workgroups of the split holding the row's last block write
-    // the new token of their KV head (wave 0 K, wave 1 V; an FP8 group is re-encoded whole)
-    // before any wave loads that block. The token is the row's last, so no other split reads
-    // its block. The row's K/V rows are read only here, after the write, so the workgroup
-    // fences and barrier are all the ordering needed.
-    if (a.write_block != nullptr && first + count == nblocks) {
-        if (wave < 2) {
-            const uint32_t kind = wave;
-            const uint32_t block = uint32_t(a.write_block[uint64_t(seq) * a.write_stride]);
-            const uint32_t slot = uint32_t(a.write_slot[uint64_t(seq) * a.write_stride]);
-            const uint16_t* fresh = (kind == 0 ? a.k_new : a.v_new) + (uint64_t(seq) * a.kv_heads + kv_head) * kDim;
-            uint8_t* base = const_cast<uint8_t*>(a.pool) + uint64_t(block) * a.block_bytes;  // the pool is written only here
-            const uint64_t group = (uint64_t(kind) * a.layers + a.layer) * a.kv_heads + kv_head;
-            if constexpr (KV == LK_BF16) {
-                if (lane < 16) {
-                    const u32x4 w = reinterpret_cast<const u32x4*>(fresh)[lane];
-                    reinterpret_cast<u32x4*>(base + (group * kSlots + slot) * kDim * kElem)[lane] = w;
-                }
-            } else {
-                u32x4 row[4];
-#pragma unroll
-                for (int j = 0; j < 4; ++j) row[j] = reinterpret_cast<const u32x4*>(fresh + 32 * (lane % 4))[j];
-                append_group_2048(base + group * kFastGroup, reinterpret_cast<int16_t*>(base + block_elems + 2 * group), slot, row, lane);
+    // the new token of their KV head (wave 0 K, wave 1 V; an FP8 group is re-encoded whole).
+    // The token is the row's last, so no other split reads its block, and in this split only
+    // the last unit does. That unit is left out of the streaming loop: every wave streams the
+    // other units meanwhile, then a workgroup barrier (with release/acquire fences) orders
+    // the write before the one wave that owns the last unit reads it. The write's latency is
+    // thus hidden behind the split's other units instead of holding every wave back.
+    const bool writes = a.write_block != nullptr && first + count == nblocks;
+    if (writes && wave < 2) {
+        const uint32_t kind = wave;
+        const uint32_t block = uint32_t(a.write_block[uint64_t(seq) * a.write_stride]);
+        const uint32_t slot = uint32_t(a.write_slot[uint64_t(seq) * a.write_stride]);
+        const uint16_t* fresh = (kind == 0 ? a.k_new : a.v_new) + (uint64_t(seq) * a.kv_heads + kv_head) * kDim;
+        uint8_t* base = const_cast<uint8_t*>(a.pool) + uint64_t(block) * a.block_bytes;  // the pool is written only here
+        const uint64_t group = (uint64_t(kind) * a.layers + a.layer) * a.kv_heads + kv_head;
+        if constexpr (KV == LK_BF16) {
+            if (lane < 16) {
+                const u32x4 w = reinterpret_cast<const u32x4*>(fresh)[lane];
+                reinterpret_cast<u32x4*>(base + (group * kSlots + slot) * kDim * kElem)[lane] = w;
             }
+        } else {
+            u32x4 row[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) row[j] = reinterpret_cast<const u32x4*>(fresh + 32 * (lane % 4))[j];
+            append_group_2048(base + group * kFastGroup, reinterpret_cast<int16_t*>(base + block_elems + 2 * group), slot, row, lane);
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        __syncthreads();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     }
+    const uint32_t streamed = writes ? count - 1 : count;  // units of the streaming loop
 
     // The block ids (and FP8 shifts) of this wave's units, one unit per lane (at most 64:
     // blocks per split <= 256), held before any tile is loaded and read back with v_readlane,
     // so no load inside the main loop has to wait for the tile loads issued ahead of it.
-    const uint32_t mine = count > wave ? (count - wave + kDecodeWaves - 1) / kDecodeWaves : 0;
+    const uint32_t mine = streamed > wave ? (streamed - wave + kDecodeWaves - 1) / kDecodeWaves : 0;
     const int32_t my_block = lane < mine ? listed_block : 0;
     int32_t my_k_shift = 0, my_v_shift = 0;
     if constexpr (KV == LK_FP8_RECORD) {
@@ -342,8 +348,7 @@ __global__ __launch_bounds__(kWave* kDecodeWaves) void decode_split_mfma(DecodeA
         }
     }
 
-    auto fetch = [&](MfmaTile<KV>& tile, uint32_t i) {
-        const int32_t block = __builtin_amdgcn_readlane(my_block, i);
+    auto fetch_block = [&](MfmaTile<KV>& tile, int32_t block, int32_t k_shift, int32_t v_shift) __attribute__((always_inline)) {
         const uint8_t* base = a.pool + uint64_t(uint32_t(block)) * a.block_bytes;
         if constexpr (KV == LK_BF16) {
 #pragma unroll
@@ -371,9 +376,13 @@ __global__ __launch_bounds__(kWave* kDecodeWaves) void decode_split_mfma(DecodeA
                 tile.v[r][0] = w[0];
                 tile.v[r][1] = w[1];
             }
-            tile.k_shift = __builtin_amdgcn_readlane(my_k_shift, i);
-            tile.v_shift = __builtin_amdgcn_readlane(my_v_shift, i);
+            tile.k_shift = k_shift;
+            tile.v_shift = v_shift;
         }
+    };
+    auto fetch = [&](MfmaTile<KV>& tile, uint32_t i) __attribute__((always_inline)) {
+        fetch_block(tile, __builtin_amdgcn_readlane(my_block, i), __builtin_amdgcn_readlane(my_k_shift, i),
+                    __builtin_amdgcn_readlane(my_v_shift, i));
     };
 
     // Online-softmax state: lane (g, n) tracks head n over slots 4g..4g+3 of every unit (the
@@ -522,10 +531,31 @@ __global__ __launch_bounds__(kWave* kDecodeWaves) void decode_split_mfma(DecodeA
         }
     }
 
+    // The written block, last unit of the split, once every wave has passed the barrier that
+    // orders the write before it. Its FP8 shifts are read only now, after the re-encode.
+    if (writes) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __syncthreads();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        const uint32_t t = count - 1;
+        if (wave == t % kDecodeWaves) {
+            const int32_t block = __builtin_amdgcn_readlane(listed_block, (t - wave) / kDecodeWaves);
+            int32_t k_shift = 0, v_shift = 0;
+            if constexpr (KV == LK_FP8_RECORD) {
+                const int16_t* shifts = reinterpret_cast<const int16_t*>(a.pool + uint64_t(uint32_t(block)) * a.block_bytes + block_elems);
+                k_shift = __builtin_amdgcn_readfirstlane(int32_t(shifts[head_tile]));
+                v_shift = __builtin_amdgcn_readfirstlane(int32_t(shifts[uint64_t(a.layers) * a.kv_heads + head_tile]));
+            }
+            MfmaTile<KV> tile;
+            fetch_block(tile, block, k_shift, v_shift);
+            consume(tile, t);
+        }
+    }
+
     // This wave's state per head: l summed over the four lane groups; o to LDS by head, dim.
-    __shared__ float s_acc[kDecodeWaves][kMaxHeads][kDim];
-    __shared__ float s_m[kDecodeWaves][kMaxHeads];
-    __shared__ float s_l[kDecodeWaves][kMaxHeads];
+    __shared__ float s_acc[kDecodeWaves][kHeads][kDim];
+    __shared__ float s_m[kDecodeWaves][kHeads];
+    __shared__ float s_l[kDecodeWaves][kHeads];
     l += __shfl_xor(l, 16, kWave);
     l += __shfl_xor(l, 32, kWave);
     if (g == 0 && n < groups) {

@@ -110,6 +110,14 @@ uint32_t env_order() {
     return value;
 }
 
+uint32_t env_waves() {
+    static const uint32_t value = [] {
+        const char* text = getenv("LAYOVER_DECODE_WAVES");
+        return text ? uint32_t(strtoul(text, nullptr, 10)) : 0u;
+    }();
+    return value;
+}
+
 uint32_t env_bps() {
     static const uint32_t value = [] {
         const char* text = getenv("LAYOVER_DECODE_BPS");
@@ -170,15 +178,33 @@ uint64_t workspace_bytes(const lk_decode_shape& s) {
     return uint64_t(s.batch) * s.query_heads * g.splits * (uint64_t(s.head_dim) + 2) * sizeof(float);
 }
 
+// Waves per workgroup of the matrix-core kernel: 4 when the grid gives the CUs two or more
+// workgroups each; otherwise 8 (at most 8 query heads per KV head), so the few workgroups
+// still put two waves on each SIMD. (16 waves would leave each 128 registers, and the kernel
+// needs more.) LAYOVER_DECODE_WAVES=4|8 forces a count the head group allows.
+uint32_t compute_units();
+
+uint32_t decode_waves(const DecodeArgs& a, uint64_t grid) {
+    const uint32_t forced = env_waves();
+    if (forced == 4 || (forced == 8 && a.groups <= 8)) return forced;
+    if (grid >= 2ull * compute_units()) return 4;
+    return a.groups <= 8 ? 8 : 4;
+}
+
+template <int KV, int QF>
+void launch_split_mfma(const DecodeArgs& a, uint32_t grid, hipStream_t stream) {
+    const uint32_t waves = decode_waves(a, grid);
+    if (waves == 8) hipLaunchKernelGGL((decode_split_mfma<KV, QF, 8>), dim3(grid), dim3(kWave * 8), 0, stream, a);
+    else hipLaunchKernelGGL((decode_split_mfma<KV, QF, 4>), dim3(grid), dim3(kWave * 4), 0, stream, a);
+}
+
 template <int QF>
 void launch_decode(const DecodeArgs& a, const Geometry& g, int kv, void* out, hipStream_t stream) {
     if (g.fast) {
         const uint64_t grid = uint64_t(a.batch) * g.splits * a.kv_heads;
         require(grid <= 0x7FFFFFFFull, "decode grid too large");
-        if (kv == LK_BF16)
-            hipLaunchKernelGGL((decode_split_mfma<LK_BF16, QF>), dim3(uint32_t(grid)), dim3(kWave * kDecodeWaves), 0, stream, a);
-        else
-            hipLaunchKernelGGL((decode_split_mfma<LK_FP8_RECORD, QF>), dim3(uint32_t(grid)), dim3(kWave * kDecodeWaves), 0, stream, a);
+        if (kv == LK_BF16) launch_split_mfma<LK_BF16, QF>(a, uint32_t(grid), stream);
+        else launch_split_mfma<LK_FP8_RECORD, QF>(a, uint32_t(grid), stream);
     } else {
         const uint64_t grid = uint64_t(a.batch) * a.query_heads * g.splits;
         require(grid <= 0x7FFFFFFFull, "decode grid too large");

@@ -86,7 +86,7 @@ def test_graph_bookkeeping_reserves_a_scratch_block_and_pads_with_it():
     graphs.release()
     assert cache.allocator.num_used == 0
     assert graphs.q.shape == (2, 4, 4, 24) and graphs.k_new.shape == (2, 4, 2, 24)
-    assert set(graphs._workspaces) == {1, 2, 4}
+    assert graphs.widths == [7] and set(graphs._workspaces) == {(1, 7), (2, 7), (4, 7)}
 
 
 def test_graphs_decline_batches_and_tables_they_were_not_captured_for():

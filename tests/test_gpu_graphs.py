@@ -227,6 +227,39 @@ def test_graph_replays_equal_the_eager_step_and_the_oracle(fp8):
     assert graphs.run([BlockTable(ids[:21], 21 * 16)], q[:, :1], k_new[:, :1], v_new[:, :1]) is None  # wider than captured
 
 
+def test_graphs_replay_the_narrowest_width_the_rows_fit():
+    """A graph set captured for 256-block tables also holds 128- and 64-block captures; rows of
+    at most 70 blocks replay the 128-block one (a narrower view of the same packed rows), which
+    equals its eager step bit for bit and the oracle on the written pool."""
+    from layover_amd.config import ModelConfig
+    from layover_amd.kv.decode_graphs import DecodeAttentionGraphs
+    from layover_amd.kv.paged_cache import BlockTable, PagedKVCache
+
+    cfg = ModelConfig.qwen3_4b()
+    cache = PagedKVCache(cfg, 300, device="cuda", fill=False)
+    rng = np.random.default_rng(9)
+    cache.pool.copy_(torch.from_numpy(oracle.bf16_bits(rng.standard_normal(cache.pool.shape, dtype=np.float32)).view(np.int16)).cuda()
+                     .view(torch.bfloat16))
+    graphs = DecodeAttentionGraphs(cache, 32, sizes=(2,), max_tokens=16 * 256)
+    assert graphs.widths == [256, 128, 64]
+    ids = [b for b in rng.permutation(300).tolist() if b not in graphs.scratch_blocks]
+    tables = [BlockTable(ids[:70], 70 * 16 - 3), BlockTable(ids[70:100], 30 * 16)]
+    assert graphs.width_for(tables) == 128
+    q = torch.randn(36, 2, 32, 128, device="cuda").to(torch.bfloat16)
+    k_new = torch.randn(36, 2, 8, 128, device="cuda").to(torch.bfloat16)
+    v_new = torch.randn(36, 2, 8, 128, device="cuda").to(torch.bfloat16)
+    print("graphs at width 128 of 256", flush=True)
+    out = graphs.run(tables, q, k_new, v_new)
+    torch.cuda.synchronize()
+    eager = graphs.step_eager(2, 128)
+    torch.cuda.synchronize()
+    assert torch.equal(eager.view(torch.int16), out.view(torch.int16))
+    state = cache.pool.view(torch.int16).cpu().numpy().view(np.uint16)
+    rows = cache.decode_rows(tables, graphs.width).numpy()
+    assert_close(out, decode_reference(state, q.float().cpu().numpy(), rows, 4))
+    graphs.release()
+
+
 @pytest.mark.parametrize("lengths", [[1], [16 * 64], [16 * 64 + 1], [32768], [5, 16 * 300, 17, 16 * 64 * 3 + 9]],
                          ids=["one_token", "one_split", "two_splits", "batch1_32k", "mixed"])
 def test_combine_over_split_counts(lengths):
