@@ -392,7 +392,7 @@ def decode_bench(device, pool, lengths, steps: int, warmup: int, seed: int, dist
     else:
         kv_bytes = blocks * QWEN["kv_heads"] * 2 * tile * 2
     other = q.numel() * 2 * 2 + table.numel() * 4 + batch * 4
-    return {
+    result = {
         "batch": batch,
         "per_layer_us": per_layer_ms * 1e3,
         "kv_bytes_per_layer": kv_bytes,
@@ -400,6 +400,29 @@ def decode_bench(device, pool, lengths, steps: int, warmup: int, seed: int, dist
         "frac_of_hbm_peak": (kv_bytes + other) / (per_layer_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "distinct_blocks": distinct,
     }
+    if kv_pool is None:
+        # The same tiles read in the same order with no compute (lk_tile_probe): the ceiling
+        # of this access pattern on this pool, which the decode kernel is compared with.
+        from layover_amd.kernels import _lib
+
+        lib = _lib.load()
+        sink = torch.zeros(1, dtype=torch.int32, device=device)
+        stream = _lib.current_stream(device)
+        shapes = [hip_decode.decode_shape(q, pool, layer, table, groups, lens) for layer in range(QWEN["layers"])]
+        probe = lambda: [_lib.check(lib.lk_tile_probe(sh, pool.data_ptr(), table.data_ptr(), lens.data_ptr(), sink.data_ptr(), stream))
+                         for sh in shapes]
+        probe()
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(steps):
+            probe()
+        end.record()
+        end.synchronize()
+        probe_ms = start.elapsed_time(end) / (steps * QWEN["layers"])
+        result["tile_probe_us"] = probe_ms * 1e3
+        result["tile_probe_gbs"] = kv_bytes / (probe_ms * 1e-3) / 1e9
+        result["frac_of_tile_probe"] = probe_ms / per_layer_ms
+    return result
 
 
 def decode_step_events(device, pool, table, lens, q, out, workspace, groups):

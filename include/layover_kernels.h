@@ -203,6 +203,14 @@ int lk_stream_probe(const void* src, void* dst, uint64_t bytes, uint32_t* sink, 
  * mix of reads and writes; LK_ERR_INVALID for any other ratio. */
 int lk_stream_probe_mix(const void* src, uint64_t src_bytes, void* dst, uint64_t dst_bytes, void* stream);
 
+/* No counterpart in the reference; measurement only. Reads the K and V tiles that
+ * lk_paged_decode would read for `shape` (BF16 pool, 16 slots x 128 dims) and nothing else, in
+ * the decode's order: the read rate of the decode's own access pattern on a given pool and
+ * table, the ceiling the decode kernel is compared with. Writes *sink only if the data hash
+ * to a value chosen never to occur. */
+int lk_tile_probe(const lk_decode_shape* shape, const void* pool, const int32_t* table, const int32_t* lengths, void* sink,
+                  void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -235,8 +235,14 @@ __device__ __forceinline__ bool decode_unit_of(const DecodeArgs& a, uint32_t w, 
 // streaming tiles and each wave a shorter chain of dependent loads. The LDS merge keeps
 // kWaves * kHeads * kDim floats, 32 KiB either way: 8 waves hold at most 8 query heads per
 // KV head, 4 waves 16.
+// FP8 pools ask the compiler for at least two waves per SIMD (amdgpu_waves_per_eu): its
+// register allocation then comes out at 166 rather than 204, so three waves fit per SIMD, and
+// the FP8 kernel went from 170 to 152 us per layer at batch 32 (0.79 -> 0.89 of 8 TB/s) and
+// from 84.5 to 76 us at batch 64 @ 4,096 (measured on MI355X, A/B in one process). For BF16
+// pools the same request, or three or four waves with a one-tile ring, measured no faster.
 template <int KV, int QF, int kWaves = kDecodeWaves>
-__global__ __launch_bounds__(kWave* kWaves) void decode_split_mfma(DecodeArgs a) {
+__global__ __launch_bounds__(kWave* kWaves) __attribute__((amdgpu_waves_per_eu(KV == LK_FP8_RECORD ? 2 : 1))) void decode_split_mfma(
+    DecodeArgs a) {
     constexpr uint32_t kDecodeWaves = kWaves;
     constexpr uint32_t kHeads = kMaxHeads * 4 / kWaves;
     const uint32_t lane = threadIdx.x % kWave;

@@ -256,6 +256,33 @@ __global__ __launch_bounds__(256) void stream_probe(const u32x4* __restrict__ sr
     }
 }
 
+// Tile probe: reads exactly the K and V tiles a decode launch of this shape reads from a BF16
+// pool (16 x 128 tiles, 4 KiB each), in the decode kernel's order (KV head fastest, then the
+// row's blocks, then the rows), one wave per (row, block, KV head), and does nothing with
+// them: the read rate of the decode's access pattern on this pool, with no compute. Like
+// the decode, each wave first loads its row's length and block id.
+__global__ __launch_bounds__(256) void tile_probe(const uint8_t* __restrict__ pool, uint64_t block_bytes, const int32_t* __restrict__ table,
+                                                  uint32_t table_stride, const int32_t* __restrict__ lengths, uint32_t lengths_stride,
+                                                  uint32_t batch, uint32_t width, uint32_t kv_heads, uint32_t layers, uint32_t layer,
+                                                  uint32_t* __restrict__ sink) {
+    const uint64_t unit = uint64_t(blockIdx.x) * 4 + threadIdx.x / kWave;
+    const uint32_t lane = threadIdx.x % kWave;
+    const uint32_t kv = uint32_t(unit % kv_heads);
+    const uint32_t j = uint32_t((unit / kv_heads) % width);
+    const uint64_t seq = unit / (uint64_t(kv_heads) * width);
+    if (seq >= batch) return;
+    const uint32_t nblocks = blocks_of(lengths[seq * lengths_stride], kSlots);
+    if (j >= nblocks) return;
+    const uint8_t* base = pool + uint64_t(uint32_t(table[seq * table_stride + j])) * block_bytes;
+    constexpr uint64_t kTile = uint64_t(kSlots) * kDim * 2;
+    const u32x4* k = reinterpret_cast<const u32x4*>(base + (uint64_t(layer) * kv_heads + kv) * kTile);
+    const u32x4* v = reinterpret_cast<const u32x4*>(base + ((uint64_t(layers) + layer) * kv_heads + kv) * kTile);
+    u32x4 w = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w ^= __builtin_nontemporal_load(k + i * kWave + lane) ^ __builtin_nontemporal_load(v + i * kWave + lane);
+    if ((w[0] ^ w[1] ^ w[2] ^ w[3]) == 0x9E3779B9u) *sink = 1;
+}
+
 // One token per sequence written into an FP8-record pool (lk_fp8_append). One wave per
 // (row, kind, KV head) group: element e of the group (slot e / head_dim) becomes the old
 // value decoded at the old shift for slots before the write slot, the new BF16 value at the
@@ -815,6 +842,26 @@ LK_EXPORT int lk_stream_probe(const void* src, void* dst, uint64_t bytes, uint32
         const auto in = static_cast<const lk::u32x4*>(src);
         if (dst == nullptr) hipLaunchKernelGGL((lk::stream_probe<4, 0>), dim3(uint32_t(grid)), dim3(256), 0, s, in, nullptr, bytes / 16, sink);
         else hipLaunchKernelGGL((lk::stream_probe<4, 4>), dim3(uint32_t(grid)), dim3(256), 0, s, in, static_cast<lk::u32x4*>(dst), bytes / 16, sink);
+    });
+}
+
+LK_EXPORT int lk_tile_probe(const lk_decode_shape* shape, const void* pool, const int32_t* table, const int32_t* lengths, void* sink,
+                            void* stream) {
+    return lk::guarded([&] {
+        lk::require(shape != nullptr && pool != nullptr && table != nullptr && lengths != nullptr && sink != nullptr,
+                    "null shape, pool, table, lengths or sink");
+        const lk_decode_shape& s = *shape;
+        lk::check_shape(s);
+        lk::require(s.kv_format == LK_BF16 && s.slots == lk::kSlots && s.head_dim == lk::kDim, "the tile probe reads BF16 16 x 128 tiles");
+        const uint32_t table_stride = s.table_stride != 0 ? s.table_stride : s.table_width;
+        const uint32_t lengths_stride = s.lengths_stride != 0 ? s.lengths_stride : 1;
+        const uint64_t waves = uint64_t(s.batch) * s.table_width * s.kv_heads;
+        const uint64_t grid = (waves + 3) / 4;
+        lk::require(grid <= 0x7FFFFFFFull, "too many tiles for one launch");
+        hipLaunchKernelGGL(lk::tile_probe, dim3(uint32_t(grid)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                           static_cast<const uint8_t*>(pool), lk::pool_block_bytes(s), table, table_stride, lengths, lengths_stride, s.batch,
+                           s.table_width, s.kv_heads, s.layers, s.layer, static_cast<uint32_t*>(sink));
+        lk::require(hipGetLastError() == hipSuccess, "tile_probe launch failed");
     });
 }
 

@@ -73,6 +73,7 @@ SIGNATURES = {
     "lk_paged_decode_static": (c_int, [POINTER(DecodeShape), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "lk_stream_probe": (c_int, [c_void_p, c_void_p, c_uint64, c_void_p, c_void_p]),
     "lk_stream_probe_mix": (c_int, [c_void_p, c_uint64, c_void_p, c_uint64, c_void_p]),
+    "lk_tile_probe": (c_int, [POINTER(DecodeShape), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "lk_paged_prefill": (c_int, [POINTER(PrefillShape), c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_void_p]),
     "lk_paged_prefill_workspace": (c_uint64, [POINTER(PrefillShape)]),
     "lk_paged_prefill_split": (c_int, [POINTER(PrefillShape), c_void_p, c_void_p, c_void_p, c_uint32, c_void_p, c_void_p, c_uint64, c_void_p]),

@@ -47,7 +47,7 @@ def test_kernel_library_exports_every_declared_symbol():
     assert names == {"lk_abi_version", "lk_last_error", "lk_fp8_quantize", "lk_fp8_dequantize", "lk_fp8_encode",
                      "lk_fp8_decode", "lk_paged_decode_workspace", "lk_paged_decode", "lk_stream_probe", "lk_fp8_append", "lk_kv_write",
                      "lk_paged_prefill", "lk_paged_prefill_workspace", "lk_paged_prefill_split", "lk_stream_probe_mix", "lk_paged_decode_append",
-                     "lk_paged_decode_static"}
+                     "lk_paged_decode_static", "lk_tile_probe"}
     assert names <= exported(path)
     assert set(_lib.SIGNATURES) | {"lk_abi_version", "lk_last_error"} == names
 

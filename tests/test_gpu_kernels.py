@@ -478,3 +478,22 @@ def test_decode_combine_paths_match_the_oracle(hip_decode, case):
     hip_decode.run_kernel(q_gpu, pool_gpu, 0, table_gpu, lens_gpu, 4, out, workspace)
     torch.cuda.synchronize()
     assert_close_to_oracle(out, expected, case)
+
+
+def test_tile_probe_reads_without_writing_and_refuses_other_formats(hip_decode):
+    """lk_tile_probe reads the decode's tiles (a measurement probe): the sink stays zero, and a
+    pool that is not BF16 16 x 128 tiles is refused before launch."""
+    from layover_amd.kernels import _lib
+
+    lib = _lib.load()
+    q, pool, table, lens = decode_case([40, 700], layers=3, kv_heads=8, slots=16, head_dim=128, groups=4, seed=44)
+    q_gpu, pool_gpu = to_gpu_bf16(q), to_gpu_bf16(pool)
+    table_gpu, lens_gpu = torch.from_numpy(table).cuda(), torch.from_numpy(lens).cuda()
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    shape = hip_decode.decode_shape(q_gpu, pool_gpu, 2, table_gpu, 4, lens_gpu)
+    stream = _lib.current_stream(q_gpu.device)
+    _lib.check(lib.lk_tile_probe(shape, pool_gpu.data_ptr(), table_gpu.data_ptr(), lens_gpu.data_ptr(), sink.data_ptr(), stream))
+    torch.cuda.synchronize()
+    assert int(sink.item()) == 0
+    wrong = hip_decode.decode_shape(q_gpu.float(), pool_gpu.float(), 2, table_gpu, 4, lens_gpu)
+    assert lib.lk_tile_probe(wrong, pool_gpu.data_ptr(), table_gpu.data_ptr(), lens_gpu.data_ptr(), sink.data_ptr(), stream) == _lib.LK_ERR_INVALID
