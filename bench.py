@@ -669,6 +669,35 @@ def distinct_decode(device, steps: int) -> dict:
     return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in run.items()}
 
 
+def decode_scan(device) -> list:
+    """Batch-1 decode at 1,024 ... 131,072 tokens (distinct blocks, BF16 and FP8 records): how
+    the per-layer time splits into a fixed cost and a bandwidth part (`--decode-scan`)."""
+    import torch
+
+    from layover_amd.config import ModelConfig
+    from layover_amd.kernels.fp8 import Fp8Layout, quantize_blocks
+    from layover_amd.kernels.hip_decode import Fp8KVPool
+    from layover_amd.kv.paged_cache import PagedKVCache
+
+    blocks = 8192 + 64
+    cache = PagedKVCache(ModelConfig.qwen3_4b(), blocks, device=device, fill=False)
+    fill_pool(cache.pool, seed=0)
+    layout = Fp8Layout.from_cache(cache)
+    records = torch.empty(blocks, layout.record_bytes, dtype=torch.uint8, device=device)
+    for first in range(0, blocks, 512):
+        quantize_blocks(cache.pool, torch.arange(first, min(blocks, first + 512), dtype=torch.int32, device=device),
+                        records[first:].reshape(-1), layout)
+    fp8 = Fp8KVPool(records, QWEN["layers"], QWEN["kv_heads"], QWEN["slots"], QWEN["head_dim"])
+    rows = []
+    for tokens in (1024, 4096, 16384, 32768, 65536, 131072):
+        bf16 = decode_bench(device, cache.pool, [tokens], 20, 2, seed=4, distinct=True)
+        f8 = decode_bench(device, cache.pool, [tokens], 20, 2, seed=4, distinct=True, kv_pool=fp8)
+        rows.append({"tokens": tokens, "bf16_us": round(bf16["per_layer_us"], 2), "bf16_frac": round(bf16["frac_of_hbm_peak"], 4),
+                     "bf16_tile_probe_us": round(bf16["tile_probe_us"], 2), "fp8_us": round(f8["per_layer_us"], 2),
+                     "fp8_frac": round(f8["frac_of_hbm_peak"], 4)})
+    return rows
+
+
 def host_cores() -> int:
     return len(os.sched_getaffinity(0))
 
@@ -792,6 +821,7 @@ def main() -> None:
     parser.add_argument("--skip-overlap", action="store_true")
     parser.add_argument("--skip-distinct", action="store_true")
     parser.add_argument("--skip-graphs", action="store_true", help="skip the HIP-graph decode steps (rocprofv3 --pmc cannot follow replays)")
+    parser.add_argument("--decode-scan", action="store_true", help="run only the batch-1 decode scan over context lengths and print it")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this KV data path has no multi-GPU step (--gpus {args.gpus} refused)", file=sys.stderr)
@@ -807,6 +837,9 @@ def main() -> None:
 
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+    if args.decode_scan:
+        print(json.dumps({"decode_scan": decode_scan(device)}), flush=True)
+        return
     config = ModelConfig.qwen3_4b()
     block_bytes = 2 * config.num_hidden_layers * config.num_key_value_heads * 16 * config.head_dim * 2
     pool_blocks = POOL_BYTES // block_bytes
