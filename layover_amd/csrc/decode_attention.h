@@ -116,6 +116,9 @@ struct DecodeArgs {
     uint32_t write_stride;
     const uint16_t* k_new;
     const uint16_t* v_new;
+    // Non-null when every row fits one split (splits == 1, matrix-core kernel): that split's
+    // state is the answer, so the split kernel writes the output here and no combine runs.
+    void* out;
 };
 
 __device__ __forceinline__ uint32_t blocks_of(int32_t length, uint32_t slots) { return (uint32_t(length) + slots - 1) / slots; }
@@ -299,9 +302,11 @@ __global__ __launch_bounds__(kWave* kWaves) __attribute__((amdgpu_waves_per_eu(K
         }
     }
 
-    // q, the ids and the length are in flight together; only now is the length needed.
+    // q, the ids and the length are in flight together; only now is the length needed. With
+    // the output written here (one split), a row of no tokens still writes it (NaN, as the
+    // combine would).
     const uint32_t nblocks = blocks_of(length, kSlots);
-    if (first >= nblocks) return;
+    if (first >= nblocks && a.out == nullptr) return;
     const uint32_t count = min(a.bps, nblocks - first);
 
     constexpr uint32_t kElem = KV == LK_FP8_RECORD ? 1 : 2;
@@ -318,7 +323,7 @@ __global__ __launch_bounds__(kWave* kWaves) __attribute__((amdgpu_waves_per_eu(K
     // other units meanwhile, then a workgroup barrier (with release/acquire fences) orders
     // the write before the one wave that owns the last unit reads it. The write's latency is
     // thus hidden behind the split's other units instead of holding every wave back.
-    const bool writes = a.write_block != nullptr && first + count == nblocks;
+    const bool writes = a.write_block != nullptr && count > 0 && first + count == nblocks;
     if (writes && wave < 2) {
         const uint32_t kind = wave;
         const uint32_t block = uint32_t(a.write_block[uint64_t(seq) * a.write_stride]);
@@ -589,6 +594,17 @@ __global__ __launch_bounds__(kWave* kWaves) __attribute__((amdgpu_waves_per_eu(K
             const float weight = merge_weight(s_m[w][h], best);
             sum += s_acc[w][h][d] * weight;
             lsum += s_l[w][h] * weight;
+        }
+        if (a.out != nullptr) {
+            // The row's only split: the combine's arithmetic for one split (weight 1, its sum
+            // starting from +0, so a -0 becomes +0 there too), times the reciprocal of l, so
+            // results equal the two-launch form bit for bit.
+            const uint64_t at = (uint64_t(seq) * a.query_heads + kv_head * groups + h) * kDim + d;
+            const float inverse = 1.0f / lsum;
+            const float merged = sum + 0.0f;
+            if constexpr (QF == LK_BF16) reinterpret_cast<uint16_t*>(a.out)[at] = to_bf16(merged * inverse);
+            else reinterpret_cast<float*>(a.out)[at] = merged * inverse;
+            continue;
         }
         const uint64_t slot = (uint64_t(seq) * a.query_heads + kv_head * groups + h) * a.splits + split;
         a.partial_acc[slot * kDim + d] = sum;

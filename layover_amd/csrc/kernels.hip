@@ -110,6 +110,9 @@ uint32_t env_order() {
     return value;
 }
 
+// Read at every launch (a getenv is far cheaper than a launch), so tests can compare both forms.
+uint32_t env_combine() { return getenv("LAYOVER_DECODE_COMBINE") != nullptr ? 1u : 0u; }
+
 uint32_t env_waves() {
     static const uint32_t value = [] {
         const char* text = getenv("LAYOVER_DECODE_WAVES");
@@ -212,6 +215,7 @@ void launch_decode(const DecodeArgs& a, const Geometry& g, int kv, void* out, hi
         else if (kv == LK_F32) hipLaunchKernelGGL((decode_split_generic<LK_F32, QF>), dim3(uint32_t(grid)), dim3(kWave), 0, stream, a);
         else hipLaunchKernelGGL((decode_split_generic<LK_FP8_RECORD, QF>), dim3(uint32_t(grid)), dim3(kWave), 0, stream, a);
     }
+    if (a.out != nullptr) return;  // the split kernel wrote the output
     const dim3 grid(a.batch * a.query_heads);
     if (!vector_combine_fits(a)) hipLaunchKernelGGL((decode_combine<QF>), grid, dim3(kWave), 0, stream, a, out);
     else if (a.splits <= kWave) hipLaunchKernelGGL((decode_combine_vector<QF, false>), grid, dim3(kWave), 0, stream, a, out);
@@ -516,6 +520,9 @@ void run_decode(const lk_decode_shape& s, const void* q, const void* pool, const
     a.vector_combine = aligned(workspace, 16) && aligned(out, s.q_format == LK_BF16 ? 8 : 16);
     a.block_bytes = pool_block_bytes(s);
     a.scale_log2 = s.scale * kLog2e;
+    // One split per row (tables of at most `bps` blocks): the split kernel writes the output.
+    // LAYOVER_DECODE_COMBINE keeps the combine launch (for comparisons).
+    if (g.fast && g.splits == 1 && env_combine() == 0) a.out = out;
     require(aligned(pool, s.kv_format == LK_F32 ? 4 : (s.kv_format == LK_BF16 ? 2 : 1)), "misaligned pool");
     if (write != nullptr) {
         require(write->write_block && write->write_slot && write->k && write->v, "null write rows, k or v");

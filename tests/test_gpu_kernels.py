@@ -497,3 +497,44 @@ def test_tile_probe_reads_without_writing_and_refuses_other_formats(hip_decode):
     assert int(sink.item()) == 0
     wrong = hip_decode.decode_shape(q_gpu.float(), pool_gpu.float(), 2, table_gpu, 4, lens_gpu)
     assert lib.lk_tile_probe(wrong, pool_gpu.data_ptr(), table_gpu.data_ptr(), lens_gpu.data_ptr(), sink.data_ptr(), stream) == _lib.LK_ERR_INVALID
+
+
+@pytest.mark.parametrize("kv", ["bf16", "fp8"])
+@pytest.mark.parametrize("q_format", ["bf16", "f32"])
+def test_decode_with_one_split_writes_the_output_itself_bit_for_bit(fp8, hip_decode, kv, q_format, monkeypatch):
+    """Tables of at most one split's blocks (here 1,024 tokens: 64 blocks) skip the combine
+    launch: the split kernel writes the output with the combine's arithmetic. Outputs equal the
+    two-launch form (LAYOVER_DECODE_COMBINE) bit for bit, including a row whose V is all -0.0
+    (the combine turns -0 into +0) and ragged rows of one token, and stay within the oracle's
+    tolerance."""
+    lengths = [1, 16, 17, 1024, 333]
+    q, pool, table, lens = decode_case(lengths, layers=2, kv_heads=2, slots=16, head_dim=128, groups=4, seed=9)
+    pool[table[1, 0], 1] = 0x8000  # row 1's only block: every V value -0.0
+    q_gpu = to_gpu_bf16(q) if q_format == "bf16" else to_gpu_bf16(q).float()
+    table_gpu, lens_gpu = torch.from_numpy(table).cuda(), torch.from_numpy(lens).cuda()
+    if kv == "bf16":
+        target, reference_pool = to_gpu_bf16(pool), pool
+    else:
+        layout = fp8.Fp8Layout(16 * 128, 2 * 2 * 2)
+        blocks = pool.shape[0]
+        records = torch.empty(blocks, layout.record_bytes, dtype=torch.uint8, device="cuda")
+        fp8.quantize_blocks(to_gpu_bf16(pool), torch.arange(blocks, dtype=torch.int32, device="cuda"), records.view(-1), layout)
+        target = hip_decode.Fp8KVPool(records, 2, 2, 16, 128)
+        reference_pool = np.zeros_like(pool)
+        oracle.dequantize_records(records.cpu().numpy().reshape(-1), np.arange(blocks, dtype=np.int32), reference_pool, layout.group_elems,
+                                  layout.groups_per_block)
+    print(f"one-split decode {kv} q {q_format}", flush=True)
+    assert int(table.shape[1]) <= 64
+    for layer in (0, 1):
+        direct = hip_decode.paged_decode_attention_hip(q_gpu, target, layer, table_gpu, lens_gpu, 4)
+        monkeypatch.setenv("LAYOVER_DECODE_COMBINE", "1")
+        combined = hip_decode.paged_decode_attention_hip(q_gpu, target, layer, table_gpu, lens_gpu, 4)
+        monkeypatch.delenv("LAYOVER_DECODE_COMBINE")
+        torch.cuda.synchronize()
+        assert torch.equal(direct.view(torch.int16) if q_format == "bf16" else direct.view(torch.int32),
+                           combined.view(torch.int16) if q_format == "bf16" else combined.view(torch.int32)), f"layer {layer}"
+        if layer == 1:
+            assert (direct[1].float() == 0).all() and not torch.signbit(direct[1].float()).any()
+        expected = oracle.decode_attention(q, reference_pool, layer, table, lens, 4)
+        weighted = weighted_mean_abs_v(q, reference_pool, layer, table, lens, 4) if kv == "fp8" else None
+        assert_close_to_oracle(direct.float(), expected, f"{kv} layer {layer}", weight_rounding=weighted)
