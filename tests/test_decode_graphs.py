@@ -3,6 +3,8 @@ quantizer, which test_oracle.py pins against the reference's codec) and the book
 DecodeAttentionGraphs (reference layover/decode_graphs.py: sizes, padding rows on a reserved
 scratch block, fixed table width). Replays themselves run in tests/test_gpu_graphs.py."""
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -213,3 +215,23 @@ def test_fp8_prefill_workspace_holds_the_staged_history(monkeypatch):
     assert lib.lk_paged_prefill_workspace(short) == 8 * 2048 * 4 * 130 * 4
     monkeypatch.delenv("LAYOVER_PREFILL_SPLITS")
     assert lib.lk_paged_prefill_workspace(long_chunk) == 0
+
+
+def test_decode_split_plan_fills_the_gpu_at_small_batch():
+    """The decode workspace follows the split plan: about 4,096 workgroups of at least 64
+    blocks at large batch, about one workgroup per CU (256 without a GPU) when that would
+    leave CUs idle, and one split for FP8-record tables of at most 64 blocks. Workspace =
+    batch x query heads x splits x (128 + 2) x 4 bytes."""
+    from layover_amd.kernels import _lib
+
+    lib = _lib.load()
+
+    def splits(batch, width, kv_format=_lib.LK_BF16):
+        shape = _lib.DecodeShape(batch, 32, 8, 128, 36, 16, 0, width, _lib.LK_BF16, kv_format, 1.0 / math.sqrt(128), 0, 0)
+        return lib.lk_paged_decode_workspace(shape) // (batch * 32 * 130 * 4)
+
+    assert splits(32, 2048) == 16  # 128-block splits: 32 x 8 x 16 = 4,096 workgroups
+    assert splits(64, 256) == 4 and splits(1, 2048) == 32  # 64-block splits
+    assert splits(1, 256) == 32 and splits(1, 1024) == 32 and splits(2, 256) == 16  # 8, 32, 16 blocks: 256 workgroups
+    assert splits(4, 256) == 8 and splits(8, 256) == 4
+    assert splits(1, 64) == 8 and splits(1, 64, _lib.LK_FP8_RECORD) == 1 and splits(1, 65, _lib.LK_FP8_RECORD) == 9
