@@ -400,28 +400,28 @@ def decode_bench(device, pool, lengths, steps: int, warmup: int, seed: int, dist
         "frac_of_hbm_peak": (kv_bytes + other) / (per_layer_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "distinct_blocks": distinct,
     }
-    if kv_pool is None:
-        # The same tiles read in the same order with no compute (lk_tile_probe): the ceiling
-        # of this access pattern on this pool, which the decode kernel is compared with.
-        from layover_amd.kernels import _lib
+    # The same tiles read in the same order with no compute (lk_tile_probe): the ceiling
+    # of this access pattern on this pool, which the decode kernel is compared with.
+    from layover_amd.kernels import _lib
 
-        lib = _lib.load()
-        sink = torch.zeros(1, dtype=torch.int32, device=device)
-        stream = _lib.current_stream(device)
-        shapes = [hip_decode.decode_shape(q, pool, layer, table, groups, lens) for layer in range(QWEN["layers"])]
-        probe = lambda: [_lib.check(lib.lk_tile_probe(sh, pool.data_ptr(), table.data_ptr(), lens.data_ptr(), sink.data_ptr(), stream))
-                         for sh in shapes]
+    lib = _lib.load()
+    sink = torch.zeros(1, dtype=torch.int32, device=device)
+    stream = _lib.current_stream(device)
+    storage = kv_pool.records if kv_pool is not None else pool
+    shapes = [hip_decode.decode_shape(q, target, layer, table, groups, lens) for layer in range(QWEN["layers"])]
+    probe = lambda: [_lib.check(lib.lk_tile_probe(sh, storage.data_ptr(), table.data_ptr(), lens.data_ptr(), sink.data_ptr(), stream))
+                     for sh in shapes]
+    probe()
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(steps):
         probe()
-        torch.cuda.synchronize()
-        start.record()
-        for _ in range(steps):
-            probe()
-        end.record()
-        end.synchronize()
-        probe_ms = start.elapsed_time(end) / (steps * QWEN["layers"])
-        result["tile_probe_us"] = probe_ms * 1e3
-        result["tile_probe_gbs"] = kv_bytes / (probe_ms * 1e-3) / 1e9
-        result["frac_of_tile_probe"] = probe_ms / per_layer_ms
+    end.record()
+    end.synchronize()
+    probe_ms = start.elapsed_time(end) / (steps * QWEN["layers"])
+    result["tile_probe_us"] = probe_ms * 1e3
+    result["tile_probe_gbs"] = kv_bytes / (probe_ms * 1e-3) / 1e9
+    result["frac_of_tile_probe"] = probe_ms / per_layer_ms
     return result
 
 
@@ -694,7 +694,7 @@ def decode_scan(device) -> list:
         f8 = decode_bench(device, cache.pool, [tokens], 20, 2, seed=4, distinct=True, kv_pool=fp8)
         rows.append({"tokens": tokens, "bf16_us": round(bf16["per_layer_us"], 2), "bf16_frac": round(bf16["frac_of_hbm_peak"], 4),
                      "bf16_tile_probe_us": round(bf16["tile_probe_us"], 2), "fp8_us": round(f8["per_layer_us"], 2),
-                     "fp8_frac": round(f8["frac_of_hbm_peak"], 4)})
+                     "fp8_frac": round(f8["frac_of_hbm_peak"], 4), "fp8_tile_probe_us": round(f8["tile_probe_us"], 2)})
     return rows
 
 

@@ -204,7 +204,8 @@ int lk_stream_probe(const void* src, void* dst, uint64_t bytes, uint32_t* sink, 
 int lk_stream_probe_mix(const void* src, uint64_t src_bytes, void* dst, uint64_t dst_bytes, void* stream);
 
 /* No counterpart in the reference; measurement only. Reads the K and V tiles that
- * lk_paged_decode would read for `shape` (BF16 pool, 16 slots x 128 dims) and nothing else, in
+ * lk_paged_decode would read for `shape` (BF16 or FP8-record pool, 16 slots x 128 dims; for
+ * FP8 records also the two groups' shifts) and nothing else, in
  * the decode's order: the read rate of the decode's own access pattern on a given pool and
  * table, the ceiling the decode kernel is compared with. Writes *sink only if the data hash
  * to a value chosen never to occur. */

@@ -271,10 +271,12 @@ __global__ __launch_bounds__(256) void stream_probe(const u32x4* __restrict__ sr
 }
 
 // Tile probe: reads exactly the K and V tiles a decode launch of this shape reads from a BF16
-// pool (16 x 128 tiles, 4 KiB each), in the decode kernel's order (KV head fastest, then the
-// row's blocks, then the rows), one wave per (row, block, KV head), and does nothing with
-// them: the read rate of the decode's access pattern on this pool, with no compute. Like
-// the decode, each wave first loads its row's length and block id.
+// pool (16 x 128 tiles, 4 KiB each) or an FP8-record pool (2 KiB tiles and the two groups'
+// shifts), in the decode kernel's order (KV head fastest, then the row's blocks, then the
+// rows), one wave per (row, block, KV head), and does nothing with them: the read rate of the
+// decode's access pattern on this pool, with no compute. Like the decode, each wave first
+// loads its row's length and block id.
+template <int KV>
 __global__ __launch_bounds__(256) void tile_probe(const uint8_t* __restrict__ pool, uint64_t block_bytes, const int32_t* __restrict__ table,
                                                   uint32_t table_stride, const int32_t* __restrict__ lengths, uint32_t lengths_stride,
                                                   uint32_t batch, uint32_t width, uint32_t kv_heads, uint32_t layers, uint32_t layer,
@@ -288,12 +290,19 @@ __global__ __launch_bounds__(256) void tile_probe(const uint8_t* __restrict__ po
     const uint32_t nblocks = blocks_of(lengths[seq * lengths_stride], kSlots);
     if (j >= nblocks) return;
     const uint8_t* base = pool + uint64_t(uint32_t(table[seq * table_stride + j])) * block_bytes;
-    constexpr uint64_t kTile = uint64_t(kSlots) * kDim * 2;
-    const u32x4* k = reinterpret_cast<const u32x4*>(base + (uint64_t(layer) * kv_heads + kv) * kTile);
-    const u32x4* v = reinterpret_cast<const u32x4*>(base + ((uint64_t(layers) + layer) * kv_heads + kv) * kTile);
+    constexpr uint64_t kTile = uint64_t(kSlots) * kDim * (KV == LK_FP8_RECORD ? 1 : 2);
+    constexpr int kWords = int(kTile / (16 * kWave));  // 16-byte words per lane and tile
+    const uint64_t k_group = uint64_t(layer) * kv_heads + kv, v_group = (uint64_t(layers) + layer) * kv_heads + kv;
+    const u32x4* k = reinterpret_cast<const u32x4*>(base + k_group * kTile);
+    const u32x4* v = reinterpret_cast<const u32x4*>(base + v_group * kTile);
     u32x4 w = {0, 0, 0, 0};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) w ^= __builtin_nontemporal_load(k + i * kWave + lane) ^ __builtin_nontemporal_load(v + i * kWave + lane);
+    for (int i = 0; i < kWords; ++i) w ^= __builtin_nontemporal_load(k + i * kWave + lane) ^ __builtin_nontemporal_load(v + i * kWave + lane);
+    if constexpr (KV == LK_FP8_RECORD) {
+        // The two groups' shifts, as the decode loads them (after the record's codes).
+        const int16_t* shifts = reinterpret_cast<const int16_t*>(base + 2 * layers * kv_heads * kTile);
+        if (lane == 0) w[0] ^= uint32_t(shifts[k_group]) ^ (uint32_t(shifts[v_group]) << 16);
+    }
     if ((w[0] ^ w[1] ^ w[2] ^ w[3]) == 0x9E3779B9u) *sink = 1;
 }
 
@@ -869,15 +878,17 @@ LK_EXPORT int lk_tile_probe(const lk_decode_shape* shape, const void* pool, cons
                     "null shape, pool, table, lengths or sink");
         const lk_decode_shape& s = *shape;
         lk::check_shape(s);
-        lk::require(s.kv_format == LK_BF16 && s.slots == lk::kSlots && s.head_dim == lk::kDim, "the tile probe reads BF16 16 x 128 tiles");
+        lk::require((s.kv_format == LK_BF16 || s.kv_format == LK_FP8_RECORD) && s.slots == lk::kSlots && s.head_dim == lk::kDim,
+                    "the tile probe reads BF16 or FP8-record 16 x 128 tiles");
         const uint32_t table_stride = s.table_stride != 0 ? s.table_stride : s.table_width;
         const uint32_t lengths_stride = s.lengths_stride != 0 ? s.lengths_stride : 1;
         const uint64_t waves = uint64_t(s.batch) * s.table_width * s.kv_heads;
         const uint64_t grid = (waves + 3) / 4;
         lk::require(grid <= 0x7FFFFFFFull, "too many tiles for one launch");
-        hipLaunchKernelGGL(lk::tile_probe, dim3(uint32_t(grid)), dim3(256), 0, static_cast<hipStream_t>(stream),
-                           static_cast<const uint8_t*>(pool), lk::pool_block_bytes(s), table, table_stride, lengths, lengths_stride, s.batch,
-                           s.table_width, s.kv_heads, s.layers, s.layer, static_cast<uint32_t*>(sink));
+        const auto kernel = s.kv_format == LK_BF16 ? lk::tile_probe<LK_BF16> : lk::tile_probe<LK_FP8_RECORD>;
+        hipLaunchKernelGGL(kernel, dim3(uint32_t(grid)), dim3(256), 0, static_cast<hipStream_t>(stream), static_cast<const uint8_t*>(pool),
+                           lk::pool_block_bytes(s), table, table_stride, lengths, lengths_stride, s.batch, s.table_width, s.kv_heads, s.layers,
+                           s.layer, static_cast<uint32_t*>(sink));
         lk::require(hipGetLastError() == hipSuccess, "tile_probe launch failed");
     });
 }

@@ -480,9 +480,9 @@ def test_decode_combine_paths_match_the_oracle(hip_decode, case):
     assert_close_to_oracle(out, expected, case)
 
 
-def test_tile_probe_reads_without_writing_and_refuses_other_formats(hip_decode):
-    """lk_tile_probe reads the decode's tiles (a measurement probe): the sink stays zero, and a
-    pool that is not BF16 16 x 128 tiles is refused before launch."""
+def test_tile_probe_reads_without_writing_and_refuses_other_formats(fp8, hip_decode):
+    """lk_tile_probe reads the decode's tiles (a measurement probe) from BF16 and FP8-record
+    pools: the sink stays zero, and an FP32 pool is refused before launch."""
     from layover_amd.kernels import _lib
 
     lib = _lib.load()
@@ -490,9 +490,16 @@ def test_tile_probe_reads_without_writing_and_refuses_other_formats(hip_decode):
     q_gpu, pool_gpu = to_gpu_bf16(q), to_gpu_bf16(pool)
     table_gpu, lens_gpu = torch.from_numpy(table).cuda(), torch.from_numpy(lens).cuda()
     sink = torch.zeros(1, dtype=torch.int32, device="cuda")
-    shape = hip_decode.decode_shape(q_gpu, pool_gpu, 2, table_gpu, 4, lens_gpu)
     stream = _lib.current_stream(q_gpu.device)
+    shape = hip_decode.decode_shape(q_gpu, pool_gpu, 2, table_gpu, 4, lens_gpu)
     _lib.check(lib.lk_tile_probe(shape, pool_gpu.data_ptr(), table_gpu.data_ptr(), lens_gpu.data_ptr(), sink.data_ptr(), stream))
+    layout = fp8.Fp8Layout(16 * 128, 2 * 3 * 8)
+    blocks = pool.shape[0]
+    records = torch.empty(blocks, layout.record_bytes, dtype=torch.uint8, device="cuda")
+    fp8.quantize_blocks(pool_gpu, torch.arange(blocks, dtype=torch.int32, device="cuda"), records.view(-1), layout)
+    fp8_pool = hip_decode.Fp8KVPool(records, 3, 8, 16, 128)
+    fp8_shape = hip_decode.decode_shape(q_gpu, fp8_pool, 2, table_gpu, 4, lens_gpu)
+    _lib.check(lib.lk_tile_probe(fp8_shape, records.data_ptr(), table_gpu.data_ptr(), lens_gpu.data_ptr(), sink.data_ptr(), stream))
     torch.cuda.synchronize()
     assert int(sink.item()) == 0
     wrong = hip_decode.decode_shape(q_gpu.float(), pool_gpu.float(), 2, table_gpu, 4, lens_gpu)
