@@ -316,34 +316,109 @@ __global__ __launch_bounds__(kWave* kWaves) __attribute__((amdgpu_waves_per_eu(K
     const uint64_t v_offset = (uint64_t(a.layers) * a.kv_heads + head_tile) * tile_bytes + (uint64_t(4 * g) * kDim + 8 * n) * kElem;
     const uint64_t block_elems = uint64_t(2) * a.layers * a.kv_heads * kSlots * kDim;  // FP8: shifts follow the data
 
-    // Fused decode-time write: the workgroups of the split holding the row's last block write
-    // the new token of their KV head (wave 0 K, wave 1 V; an FP8 group is re-encoded whole).
-    // The token is the row's last, so no other split reads its block, and in this split only
-    // the last unit does. That unit is left out of the streaming loop: every wave streams the
-    // other units meanwhile, then a workgroup barrier (with release/acquire fences) orders
-    // the write before the one wave that owns the last unit reads it. The write's latency is
-    // thus hidden behind the split's other units instead of holding every wave back.
+    // Fused decode-time write. The token is the row's last, so no other split reads its block,
+    // and in this split only the last unit does. The wave that owns that unit (round-robin)
+    // writes the token of its KV head at the start and takes the written values from its own
+    // registers when it consumes the unit, so no wave waits for the write: BF16 tiles are
+    // fetched as usual and the written slot's rows replaced by the new token (which is what
+    // memory holds once the write lands); FP8 groups are re-encoded whole, and the new codes go
+    // to LDS, where the same wave reads them back in the tile's layout, with the new shifts.
     const bool writes = a.write_block != nullptr && count > 0 && first + count == nblocks;
-    if (writes && wave < 2) {
-        const uint32_t kind = wave;
+    const uint32_t writer = writes ? (count - 1) % kDecodeWaves : kDecodeWaves;
+    constexpr bool kBf16 = KV == LK_BF16;
+    uint32_t patch_k[kBf16 ? 16 : 1] = {}, patch_v[kBf16 ? 4 : 1] = {};
+    uint32_t write_slot = 0;
+    int32_t new_k_shift = 0, new_v_shift = 0;
+    __shared__ __align__(16) uint8_t s_written[kBf16 ? 16 : 2 * kFastGroup];
+    uint8_t* write_base = nullptr;
+    u32x4 old_k[2], old_v[2], row_k[kBf16 ? 1 : 4], row_v[kBf16 ? 1 : 4];
+    int32_t old_k_shift = 0, old_v_shift = 0;
+    // With 8 waves (small grids) the writer issues its first tile loads before re-encoding, so
+    // the two sets of loads are in flight together; the 4-wave kernel re-encodes at once, which
+    // keeps the loaded values out of its main loop's registers (three waves per SIMD for FP8).
+    constexpr bool kLateEncode = !kBf16 && kWaves == 8;
+    // FP8: the two re-encodes, their codes also to LDS for the written unit's consume.
+    auto reencode = [&]() __attribute__((always_inline)) {
+        if constexpr (!kBf16) {
+            const uint64_t k_group = head_tile, v_group = uint64_t(a.layers) * a.kv_heads + head_tile;
+            int16_t* shifts = reinterpret_cast<int16_t*>(write_base + block_elems);
+            u32x4 out[2];
+            new_k_shift = append_group_2048_loaded(write_base + k_group * kFastGroup, shifts + k_group, write_slot, row_k, lane, old_k, old_k_shift, out);
+            reinterpret_cast<u32x4*>(s_written)[2 * lane] = out[0];
+            reinterpret_cast<u32x4*>(s_written)[2 * lane + 1] = out[1];
+            new_v_shift = append_group_2048_loaded(write_base + v_group * kFastGroup, shifts + v_group, write_slot, row_v, lane, old_v, old_v_shift, out);
+            reinterpret_cast<u32x4*>(s_written + kFastGroup)[2 * lane] = out[0];
+            reinterpret_cast<u32x4*>(s_written + kFastGroup)[2 * lane + 1] = out[1];
+        }
+    };
+    if (wave == writer) {
         const uint32_t block = uint32_t(a.write_block[uint64_t(seq) * a.write_stride]);
-        const uint32_t slot = uint32_t(a.write_slot[uint64_t(seq) * a.write_stride]);
-        const uint16_t* fresh = (kind == 0 ? a.k_new : a.v_new) + (uint64_t(seq) * a.kv_heads + kv_head) * kDim;
+        write_slot = uint32_t(a.write_slot[uint64_t(seq) * a.write_stride]);
+        const uint16_t* k_row = a.k_new + (uint64_t(seq) * a.kv_heads + kv_head) * kDim;
+        const uint16_t* v_row = a.v_new + (uint64_t(seq) * a.kv_heads + kv_head) * kDim;
         uint8_t* base = const_cast<uint8_t*>(a.pool) + uint64_t(block) * a.block_bytes;  // the pool is written only here
-        const uint64_t group = (uint64_t(kind) * a.layers + a.layer) * a.kv_heads + kv_head;
-        if constexpr (KV == LK_BF16) {
-            if (lane < 16) {
-                const u32x4 w = reinterpret_cast<const u32x4*>(fresh)[lane];
-                reinterpret_cast<u32x4*>(base + (group * kSlots + slot) * kDim * kElem)[lane] = w;
+        const uint64_t k_group = head_tile, v_group = uint64_t(a.layers) * a.kv_heads + head_tile;
+        if constexpr (kBf16) {
+            if (lane < 32) {
+                const u32x4 w = reinterpret_cast<const u32x4*>(lane < 16 ? k_row : v_row)[lane % 16];
+                reinterpret_cast<u32x4*>(base + ((lane < 16 ? k_group : v_group) * kSlots + write_slot) * kDim * kElem)[lane % 16] = w;
             }
-        } else {
-            u32x4 row[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) row[j] = reinterpret_cast<const u32x4*>(fresh + 32 * (lane % 4))[j];
-            append_group_2048(base + group * kFastGroup, reinterpret_cast<int16_t*>(base + block_elems + 2 * group), slot, row, lane);
+            for (int j = 0; j < 4; ++j) {
+                const u32x4 w = *reinterpret_cast<const u32x4*>(k_row + MfmaTile<KV>::kGroupDims * g + j * MfmaTile<KV>::kStepDims);
+#pragma unroll
+                for (int x = 0; x < 4; ++x) patch_k[4 * j + x] = w[x];
+            }
+            const u32x4 w = *reinterpret_cast<const u32x4*>(v_row + 8 * n);
+#pragma unroll
+            for (int x = 0; x < 4; ++x) patch_v[x] = w[x];
+        } else {
+            // Both groups' old codes, shifts and new rows are loaded before either re-encode.
+            write_base = base;
+            const u32x4* old_k_at = reinterpret_cast<const u32x4*>(base + k_group * kFastGroup) + 2 * lane;
+            const u32x4* old_v_at = reinterpret_cast<const u32x4*>(base + v_group * kFastGroup) + 2 * lane;
+            old_k[0] = old_k_at[0];
+            old_k[1] = old_k_at[1];
+            old_v[0] = old_v_at[0];
+            old_v[1] = old_v_at[1];
+            const int16_t* shifts = reinterpret_cast<const int16_t*>(base + block_elems);
+            old_k_shift = shifts[k_group];
+            old_v_shift = shifts[v_group];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                row_k[j] = reinterpret_cast<const u32x4*>(k_row + 32 * (lane % 4))[j];
+                row_v[j] = reinterpret_cast<const u32x4*>(v_row + 32 * (lane % 4))[j];
+            }
+            if constexpr (!kLateEncode) reencode();
         }
     }
-    const uint32_t streamed = writes ? count - 1 : count;  // units of the streaming loop
+    // The written unit's tile as memory holds it after the write (see above).
+    auto written = [&](MfmaTile<KV>& tile) __attribute__((always_inline)) {
+        if constexpr (kBf16) {
+#pragma unroll
+            for (int x = 0; x < 16; ++x) tile.k[x] = n == write_slot ? patch_k[x] : tile.k[x];
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int x = 0; x < 4; ++x) tile.v[r][x] = 4 * g + r == write_slot ? patch_v[x] : tile.v[r][x];
+        } else {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const u32x4 w = reinterpret_cast<const u32x4*>(s_written + n * kDim + MfmaTile<KV>::kGroupDims * g)[j];
+#pragma unroll
+                for (int x = 0; x < 4; ++x) tile.k[4 * j + x] = w[x];
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const u32x2 w = *reinterpret_cast<const u32x2*>(s_written + kFastGroup + (4 * g + r) * kDim + 8 * n);
+                tile.v[r][0] = w[0];
+                tile.v[r][1] = w[1];
+            }
+            tile.k_shift = new_k_shift;
+            tile.v_shift = new_v_shift;
+        }
+    };
+    const uint32_t streamed = count;  // units of the streaming loop
 
     // The block ids (and FP8 shifts) of this wave's units, one unit per lane (at most 64:
     // blocks per split <= 256), held before any tile is loaded and read back with v_readlane,
@@ -533,33 +608,17 @@ __global__ __launch_bounds__(kWave* kWaves) __attribute__((amdgpu_waves_per_eu(K
         const uint32_t last = mine - 1;
 #pragma unroll
         for (int d = 0; d < kRing; ++d) fetch(ring[d], min(uint32_t(d), last));
+        if (kLateEncode && wave == writer) reencode();
         for (uint32_t i = 0; i < mine; i += kRing) {
 #pragma unroll
             for (int d = 0; d < kRing; ++d) {
-                if (i + d < mine) consume(ring[d], wave + (i + d) * kDecodeWaves);
+                if (i + d < mine) {
+                    const uint32_t t = wave + (i + d) * kDecodeWaves;
+                    if (t == count - 1 && wave == writer) written(ring[d]);
+                    consume(ring[d], t);
+                }
                 fetch(ring[d], min(i + d + kRing, last));
             }
-        }
-    }
-
-    // The written block, last unit of the split, once every wave has passed the barrier that
-    // orders the write before it. Its FP8 shifts are read only now, after the re-encode.
-    if (writes) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        __syncthreads();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        const uint32_t t = count - 1;
-        if (wave == t % kDecodeWaves) {
-            const int32_t block = __builtin_amdgcn_readlane(listed_block, (t - wave) / kDecodeWaves);
-            int32_t k_shift = 0, v_shift = 0;
-            if constexpr (KV == LK_FP8_RECORD) {
-                const int16_t* shifts = reinterpret_cast<const int16_t*>(a.pool + uint64_t(uint32_t(block)) * a.block_bytes + block_elems);
-                k_shift = __builtin_amdgcn_readfirstlane(int32_t(shifts[head_tile]));
-                v_shift = __builtin_amdgcn_readfirstlane(int32_t(shifts[uint64_t(a.layers) * a.kv_heads + head_tile]));
-            }
-            MfmaTile<KV> tile;
-            fetch_block(tile, block, k_shift, v_shift);
-            consume(tile, t);
         }
     }
 

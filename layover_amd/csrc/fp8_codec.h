@@ -104,11 +104,14 @@ __device__ __forceinline__ uint32_t flush_bf16_pair(uint32_t pair) {
 // after it; the group is re-encoded at the shift of those values (fp8.py:86-137). Decode and
 // encode take the hardware converts where they are exact (as the record kernels do), else the
 // reference's integer codec.
-__device__ __forceinline__ void append_group_2048(uint8_t* group, int16_t* shift_at, uint32_t write, const u32x4 (&fresh)[4], uint32_t lane) {
+//
+// append_group_2048_loaded takes the lane's old codes and the old shift from the caller (who
+// can then load several groups at once), stores the group and returns its new codes in `out`
+// and its new shift.
+__device__ __forceinline__ int32_t append_group_2048_loaded(uint8_t* group, int16_t* shift_at, uint32_t write, const u32x4 (&fresh)[4],
+                                                            uint32_t lane, const u32x4 (&old)[2], int32_t old_shift, u32x4 (&out)[2]) {
     u32x4* codes = reinterpret_cast<u32x4*>(group) + 2 * lane;
     const uint32_t slot = lane / 4;
-    const u32x4 old[2] = {codes[0], codes[1]};
-    const int32_t old_shift = *shift_at;
 
     // The old values (lanes before the write slot): a NaN code anywhere among them, or a shift
     // whose products could leave BF16's normal range, sends the wave to the integer decode.
@@ -155,7 +158,6 @@ __device__ __forceinline__ void append_group_2048(uint8_t* group, int16_t* shift
     }
     const int32_t shift = shift_from_key(wave_max(key));
     const bool nonfinite = __any((flags & 0x80008000u) != 0);
-    u32x4 out[2];
     if (!nonfinite && shift >= -126) {
         // value * 2^-shift is exact for a normal BF16 value and stays below 2^8; the convert
         // rounds to nearest even. Subnormal inputs are flushed first; products below FP32's
@@ -179,6 +181,14 @@ __device__ __forceinline__ void append_group_2048(uint8_t* group, int16_t* shift
     codes[0] = out[0];
     codes[1] = out[1];
     if (lane == 0) *shift_at = int16_t(shift);
+    return shift;
+}
+
+__device__ __forceinline__ void append_group_2048(uint8_t* group, int16_t* shift_at, uint32_t write, const u32x4 (&fresh)[4], uint32_t lane) {
+    const u32x4* codes = reinterpret_cast<const u32x4*>(group) + 2 * lane;
+    const u32x4 old[2] = {codes[0], codes[1]};
+    u32x4 out[2];
+    append_group_2048_loaded(group, shift_at, write, fresh, lane, old, *shift_at, out);
 }
 
 // Qwen3-shaped groups (2048 values, 16-byte aligned records) run the kernels of
