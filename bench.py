@@ -354,7 +354,7 @@ def decode_tables(rng, batch: int, lengths, pool_blocks: int, distinct: bool):
     return table
 
 
-def decode_bench(device, pool, lengths, steps: int, warmup: int, seed: int, distinct: bool = False, kv_pool=None):
+def decode_bench(device, pool, lengths, steps: int, warmup: int, seed: int, distinct: bool = False, kv_pool=None, probe: bool = True):
     """Time 36 single-layer launches per step; bytes are the reference's unique accounting."""
     import numpy as np
     import torch
@@ -400,6 +400,8 @@ def decode_bench(device, pool, lengths, steps: int, warmup: int, seed: int, dist
         "frac_of_hbm_peak": (kv_bytes + other) / (per_layer_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "distinct_blocks": distinct,
     }
+    if not probe:
+        return result
     # The same tiles read in the same order with no compute (lk_tile_probe): the ceiling
     # of this access pattern on this pool, which the decode kernel is compared with.
     from layover_amd.kernels import _lib
@@ -409,13 +411,13 @@ def decode_bench(device, pool, lengths, steps: int, warmup: int, seed: int, dist
     stream = _lib.current_stream(device)
     storage = kv_pool.records if kv_pool is not None else pool
     shapes = [hip_decode.decode_shape(q, target, layer, table, groups, lens) for layer in range(QWEN["layers"])]
-    probe = lambda: [_lib.check(lib.lk_tile_probe(sh, storage.data_ptr(), table.data_ptr(), lens.data_ptr(), sink.data_ptr(), stream))
-                     for sh in shapes]
-    probe()
+    read_tiles = lambda: [_lib.check(lib.lk_tile_probe(sh, storage.data_ptr(), table.data_ptr(), lens.data_ptr(), sink.data_ptr(), stream))
+                          for sh in shapes]
+    read_tiles()
     torch.cuda.synchronize()
     start.record()
     for _ in range(steps):
-        probe()
+        read_tiles()
     end.record()
     end.synchronize()
     probe_ms = start.elapsed_time(end) / (steps * QWEN["layers"])

@@ -116,8 +116,9 @@ struct DecodeArgs {
     uint32_t write_stride;
     const uint16_t* k_new;
     const uint16_t* v_new;
-    // Non-null when every row fits one split (splits == 1, matrix-core kernel): that split's
-    // state is the answer, so the split kernel writes the output here and no combine runs.
+    // Non-null when every row fits one split (splits == 1, matrix-core kernel with 8 waves):
+    // that split's state is the answer, so the split kernel writes the output here and no
+    // combine runs.
     void* out;
 };
 
@@ -303,10 +304,12 @@ __global__ __launch_bounds__(kWave* kWaves) __attribute__((amdgpu_waves_per_eu(K
     }
 
     // q, the ids and the length are in flight together; only now is the length needed. With
-    // the output written here (one split), a row of no tokens still writes it (NaN, as the
-    // combine would).
+    // the output written here (one split; 8-wave kernels only, which small grids run), a row
+    // of no tokens still writes it (NaN, as the combine would).
     const uint32_t nblocks = blocks_of(length, kSlots);
-    if (first >= nblocks && a.out == nullptr) return;
+    constexpr bool kMayWriteOut = kWaves == 8;
+    const bool writes_out = kMayWriteOut && a.out != nullptr;
+    if (first >= nblocks && !writes_out) return;
     const uint32_t count = min(a.bps, nblocks - first);
 
     constexpr uint32_t kElem = KV == LK_FP8_RECORD ? 1 : 2;
@@ -654,7 +657,7 @@ __global__ __launch_bounds__(kWave* kWaves) __attribute__((amdgpu_waves_per_eu(K
             sum += s_acc[w][h][d] * weight;
             lsum += s_l[w][h] * weight;
         }
-        if (a.out != nullptr) {
+        if (writes_out) {
             // The row's only split: the combine's arithmetic for one split (weight 1, its sum
             // starting from +0, so a -0 becomes +0 there too), times the reciprocal of l, so
             // results equal the two-launch form bit for bit.

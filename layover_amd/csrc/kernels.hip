@@ -539,9 +539,11 @@ void run_decode(const lk_decode_shape& s, const void* q, const void* pool, const
     a.vector_combine = aligned(workspace, 16) && aligned(out, s.q_format == LK_BF16 ? 8 : 16);
     a.block_bytes = pool_block_bytes(s);
     a.scale_log2 = s.scale * kLog2e;
-    // One split per row (tables of at most `bps` blocks): the split kernel writes the output.
-    // LAYOVER_DECODE_COMBINE keeps the combine launch (for comparisons).
-    if (g.fast && g.splits == 1 && env_combine() == 0) a.out = out;
+    // One split per row (tables of at most `bps` blocks) on a grid small enough for 8-wave
+    // workgroups: the split kernel writes the output. (The 4-wave kernel has no such branch,
+    // which measurably costs the large-batch loop.) LAYOVER_DECODE_COMBINE keeps the combine
+    // launch (for comparisons).
+    if (g.fast && g.splits == 1 && env_combine() == 0 && decode_waves(a, uint64_t(s.batch) * s.kv_heads) == 8) a.out = out;
     require(aligned(pool, s.kv_format == LK_F32 ? 4 : (s.kv_format == LK_BF16 ? 2 : 1)), "misaligned pool");
     if (write != nullptr) {
         require(write->write_block && write->write_slot && write->k && write->v, "null write rows, k or v");

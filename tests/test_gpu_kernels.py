@@ -509,12 +509,14 @@ def test_tile_probe_reads_without_writing_and_refuses_other_formats(fp8, hip_dec
 @pytest.mark.parametrize("kv", ["bf16", "fp8"])
 @pytest.mark.parametrize("q_format", ["bf16", "f32"])
 def test_decode_with_one_split_writes_the_output_itself_bit_for_bit(fp8, hip_decode, kv, q_format, monkeypatch):
-    """Tables of at most one split's blocks (here 1,024 tokens: 64 blocks) skip the combine
-    launch: the split kernel writes the output with the combine's arithmetic. Outputs equal the
-    two-launch form (LAYOVER_DECODE_COMBINE) bit for bit, including a row whose V is all -0.0
-    (the combine turns -0 into +0) and ragged rows of one token, and stay within the oracle's
-    tolerance."""
-    lengths = [1, 16, 17, 1024, 333]
+    """Tables of one split (FP8 records: up to 64 blocks; BF16 on a grid this small: 8-block
+    splits, so up to 128 tokens) skip the combine launch: the split kernel writes the output
+    with the combine's arithmetic. Outputs equal the two-launch form (LAYOVER_DECODE_COMBINE)
+    bit for bit, including a row whose V is all -0.0 (the combine turns -0 into +0) and ragged
+    rows of one token, and stay within the oracle's tolerance."""
+    from layover_amd.kernels import _lib
+
+    lengths = [1, 16, 17, 1024, 333] if kv == "fp8" else [1, 16, 17, 128, 100]
     q, pool, table, lens = decode_case(lengths, layers=2, kv_heads=2, slots=16, head_dim=128, groups=4, seed=9)
     pool[table[1, 0], 1] = 0x8000  # row 1's only block: every V value -0.0
     q_gpu = to_gpu_bf16(q) if q_format == "bf16" else to_gpu_bf16(q).float()
@@ -531,7 +533,8 @@ def test_decode_with_one_split_writes_the_output_itself_bit_for_bit(fp8, hip_dec
         oracle.dequantize_records(records.cpu().numpy().reshape(-1), np.arange(blocks, dtype=np.int32), reference_pool, layout.group_elems,
                                   layout.groups_per_block)
     print(f"one-split decode {kv} q {q_format}", flush=True)
-    assert int(table.shape[1]) <= 64
+    shape = hip_decode.decode_shape(q_gpu, target, 0, table_gpu, 4, lens_gpu)
+    assert _lib.load().lk_paged_decode_workspace(shape) == len(lengths) * 8 * 130 * 4  # one split
     for layer in (0, 1):
         direct = hip_decode.paged_decode_attention_hip(q_gpu, target, layer, table_gpu, lens_gpu, 4)
         monkeypatch.setenv("LAYOVER_DECODE_COMBINE", "1")
