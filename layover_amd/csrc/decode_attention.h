@@ -28,9 +28,11 @@
 // Generic path (any slots <= 64 and head_dim <= 256, any G): one wave per (sequence, query
 //   head, split), lane d owning dims d, d+64, ...; used for shapes other than Qwen3's.
 // Combine: one wave per (sequence, query head) merges the split partials (m, l, acc) and
-//   writes the output rounded to nearest even. (Merging inside the split kernel, in the last
-//   split to finish, needs a device-scope release per workgroup; on MI355X that fence writes
-//   back the XCD's L2 and cost more than doubled the per-layer time at batch 32.)
+//   writes the output rounded to nearest even. A table of one split needs no merge: the
+//   split kernel (8-wave form) writes the output itself. (Merging inside the split kernel,
+//   in the last split to arrive, was slower both ways it was built: behind a device-scope
+//   release, which on MI355X writes back the XCD's L2, and with agent-scope partials and an
+//   agent-scope arrival count, whose chain outlasts the separate merge launch.)
 #ifndef LAYOVER_AMD_DECODE_ATTENTION_H
 #define LAYOVER_AMD_DECODE_ATTENTION_H
 
@@ -421,12 +423,11 @@ __global__ __launch_bounds__(kWave* kWaves) __attribute__((amdgpu_waves_per_eu(K
             tile.v_shift = new_v_shift;
         }
     };
-    const uint32_t streamed = count;  // units of the streaming loop
 
     // The block ids (and FP8 shifts) of this wave's units, one unit per lane (at most 64:
     // blocks per split <= 256), held before any tile is loaded and read back with v_readlane,
     // so no load inside the main loop has to wait for the tile loads issued ahead of it.
-    const uint32_t mine = streamed > wave ? (streamed - wave + kDecodeWaves - 1) / kDecodeWaves : 0;
+    const uint32_t mine = count > wave ? (count - wave + kDecodeWaves - 1) / kDecodeWaves : 0;
     const int32_t my_block = lane < mine ? listed_block : 0;
     int32_t my_k_shift = 0, my_v_shift = 0;
     if constexpr (KV == LK_FP8_RECORD) {
