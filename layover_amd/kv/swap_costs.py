@@ -1,22 +1,23 @@
 """Swap side of the placement cost model, measured through this package's transfer path.
 
 The reference prices keeping, swapping or dropping a paused session's KV from polynomials
-fitted by bench/kv_crossover.py (read by layover/agent/cost_model.py:42-95). This module
-measures the swap half of that file on MI355X, with the same protocol:
-  - one cache sized to exactly `tokens` tokens, every block round-tripped once, out in one
-    random permutation of the pool and back into another (kv_crossover.py:187-220), so the
-    copy order is unrelated to pool order, as after evictions;
-  - BF16 first, then FP8 (whose round trip changes the values), each verified: BF16 bit for
-    bit, FP8 within round_trip_bound;
-  - each repeat timed with the device synchronized on both sides (kv_crossover.py:77-82),
-    leading repeats discarded, medians kept;
-  - linear fits with non-negative coefficients, low order first (kv_crossover.py:282-299),
-    under the reference's key names: swap_out_s_coef, swap_in_s_coef, fp8_swap_out_s_coef,
-    fp8_swap_in_s_coef, with transfer = "native".
+fitted by bench/kv_crossover.py and read by layover/agent/cost_model.py:42-95. This module
+measures the swap half on MI355X and writes it under the reference's key names
+(swap_out_s_coef, swap_in_s_coef, fp8_swap_out_s_coef, fp8_swap_in_s_coef; transfer =
+"native"), seconds = c0 + c1 * tokens. What is measured, per context length:
 
-Recompute time needs the model's prefill, which this package does not have; `--merge` writes
-these swap coefficients into a cost model JSON the reference's own sweep produced, keeping
-its recompute_s_coef, so CostModel.from_json(path, transfer="native") loads the result.
+- a cache of exactly that many tokens, every block swapped out in one random order and back
+  into another (as after evictions, copy order unrelated to pool order; the reference's
+  protocol, kv_crossover.py:187-220), BF16 and then FP8;
+- each direction timed on the host with the device idle on both sides, so host-side costs
+  (pinning, launches) count, as they do for a scheduler; leading repeats are discarded and
+  the median of the rest kept;
+- every round trip checked: BF16 bit for bit, FP8 within round_trip_bound.
+
+The fit is a non-negative least-squares line (a negative term would make a long context look
+cheap once extrapolated). Recompute time needs the model's prefill, which this package does
+not have: `--merge` writes these coefficients into a cost model JSON from the reference's own
+sweep and keeps its recompute_s_coef, so CostModel.from_json(path, transfer="native") loads it.
 
     python -m layover_amd.kv.swap_costs --device cuda --out swap_costs
 """
@@ -28,11 +29,12 @@ import csv
 import json
 import statistics
 import time
-from dataclasses import asdict, dataclass
+from contextlib import contextmanager
 from pathlib import Path
 
 import numpy as np
 import torch
+from scipy.optimize import nnls
 
 from layover_amd.config import ModelConfig
 from layover_amd.kernels.fp8 import Fp8Layout, round_trip_within_bound
@@ -41,176 +43,147 @@ from layover_amd.kv.transfer import NativeBackend
 
 DEFAULT_TOKENS = [512, 1024, 2048, 4096, 8192, 16384, 32768]
 SWAP_KEYS = ("swap_out_s_coef", "swap_in_s_coef", "fp8_swap_out_s_coef", "fp8_swap_in_s_coef")
-
-
-@dataclass
-class Row:
-    tokens: int
-    blocks: int
-    bf16_bytes: int
-    fp8_bytes: int
-    swap_out_s: float
-    swap_in_s: float
-    fp8_swap_out_s: float | None
-    fp8_swap_in_s: float | None
-    cold_pins: int
-
-
-def sync(device: torch.device) -> None:
-    if device.type == "cuda":
-        torch.cuda.synchronize(device)
-
-
-def timed(device: torch.device, fn) -> float:
-    sync(device)
-    start = time.perf_counter()
-    fn()
-    sync(device)
-    return time.perf_counter() - start
-
-
-def permutation(blocks: int, seed: int) -> list[int]:
-    return torch.randperm(blocks, generator=torch.Generator().manual_seed(seed)).tolist()
+ROW_FIELDS = ("tokens", "blocks", "bf16_bytes", "fp8_bytes", "swap_out_s", "swap_in_s", "fp8_swap_out_s", "fp8_swap_in_s", "cold_pins")
 
 
 def fit_nonnegative(x: np.ndarray, y: np.ndarray, degree: int) -> list[float]:
-    """Least-squares polynomial, low order first, whose coefficients are all >= 0: a term that
-    comes out negative is dropped and the rest refitted (kv_crossover.py:282-299). A negative
-    term would let the fit call a long context cheap once extrapolated."""
-    powers = list(range(degree + 1))
-    while True:
-        design = np.stack([x.astype(np.float64) ** p for p in powers], axis=1)
-        coef = np.linalg.lstsq(design, y.astype(np.float64), rcond=None)[0]
-        if (coef >= 0).all() or len(powers) == 1:
-            break
-        powers.pop(int(np.argmin(coef)))
-    result = [0.0] * (degree + 1)
-    for power, value in zip(powers, coef):
-        result[power] = max(float(value), 0.0)
-    return result
+    """Coefficients (low order first) of the polynomial of `degree` closest to y in least
+    squares among those with no negative coefficient (Lawson-Hanson NNLS). Columns are scaled
+    to unit norm first: x^0 and x^1 over token counts differ by four orders of magnitude."""
+    x = np.asarray(x, dtype=np.float64)
+    design = np.stack([x**power for power in range(degree + 1)], axis=1)
+    norms = np.linalg.norm(design, axis=0)
+    norms[norms == 0] = 1.0
+    scaled, _ = nnls(design / norms, np.asarray(y, dtype=np.float64))
+    return [float(c) for c in scaled / norms]
 
 
-def round_trip(backend: NativeBackend, cache: PagedKVCache, fp8: bool, seed: int) -> tuple[float, float]:
-    """Every block of the cache out and back once; returns (out seconds, in seconds)."""
-    device = cache.device
-    blocks = cache.allocator.num_blocks
-    source, target = permutation(blocks, seed), permutation(blocks, seed + 1)
-    before = cache.pool[torch.tensor(source, device=device)]
-    tickets = []
+class Sweep:
+    """Swap timings for one model shape through one NativeBackend."""
 
-    def out():
-        tickets.append(backend.start_out(cache, source, fp8))
-        tickets[-1].wait()
+    def __init__(self, cfg: ModelConfig, backend: NativeBackend, device: torch.device, with_fp8: bool, repeats: int, warmup: int,
+                 seed: int):
+        self.cfg, self.backend, self.device = cfg, backend, device
+        self.with_fp8, self.repeats, self.warmup, self.seed = with_fp8, repeats, warmup, seed
 
-    def into():
-        backend.start_in(cache, target, tickets[0].payload).wait()
+    @contextmanager
+    def _stopwatch(self, into: list[float]):
+        """Appends the seconds of the block to `into`, the device drained on both sides."""
+        if self.device.type == "cuda":
+            torch.cuda.synchronize(self.device)
+        started = time.perf_counter_ns()
+        yield
+        if self.device.type == "cuda":
+            torch.cuda.synchronize(self.device)
+        into.append((time.perf_counter_ns() - started) * 1e-9)
 
-    out_s = timed(device, out)
-    in_s = timed(device, into)
-    after = cache.pool[torch.tensor(target, device=device)]
-    if fp8:
-        if not round_trip_within_bound(before, after, Fp8Layout.from_cache(cache).group_elems, ignore_nonfinite=True):
-            raise RuntimeError("KV values left the FP8 error bound across the swap round trip")
-    elif not torch.equal(before.view(torch.int16), after.view(torch.int16)):
-        raise RuntimeError("KV bytes changed across the swap round trip")
-    backend.free(tickets[0].payload)
-    return out_s, in_s
+    def _orders(self, blocks: int, draw: int) -> tuple[list[int], list[int]]:
+        rng = np.random.default_rng([self.seed, draw])
+        return rng.permutation(blocks).tolist(), rng.permutation(blocks).tolist()
 
-
-def measure(cfg: ModelConfig, tokens: int, backend: NativeBackend, device: torch.device, fp8: bool, repeats: int,
-            warmup: int, seed: int) -> Row:
-    cache = PagedKVCache(cfg, -(-tokens // 16), device, fill=False)
-    out_b, in_b, out_f, in_f = [], [], [], []
-    pins_at_start = 0
-    for i in range(warmup + repeats):
-        if i == warmup:
-            pins_at_start = backend.pin_stats().get("host_pins", 0)
-        generator = torch.Generator(device=device).manual_seed(seed + i)
-        cache.pool.copy_(torch.randn(cache.pool.shape, generator=generator, device=device, dtype=torch.float32))
-        samples = [round_trip(backend, cache, False, seed + i)]
+    def _round_trip(self, cache: PagedKVCache, fp8: bool, draw: int, outs: list[float], ins: list[float]) -> None:
+        source, target = self._orders(cache.allocator.num_blocks, draw)
+        before = cache.pool[torch.tensor(source, device=self.device)]
+        with self._stopwatch(outs):
+            offload = self.backend.start_out(cache, source, fp8)
+            offload.wait()
+        with self._stopwatch(ins):
+            self.backend.start_in(cache, target, offload.payload).wait()
+        after = cache.pool[torch.tensor(target, device=self.device)]
+        self.backend.free(offload.payload)
         if fp8:
-            samples.append(round_trip(backend, cache, True, seed + i))
-        if i >= warmup:
-            out_b.append(samples[0][0])
-            in_b.append(samples[0][1])
-            if fp8:
-                out_f.append(samples[1][0])
-                in_f.append(samples[1][1])
-    blocks = cache.allocator.num_blocks
-    layout = Fp8Layout.from_cache(cache)
-    return Row(
-        tokens=tokens,
-        blocks=blocks,
-        bf16_bytes=blocks * cache.block_bytes,
-        fp8_bytes=blocks * layout.record_bytes,
-        swap_out_s=statistics.median(out_b),
-        swap_in_s=statistics.median(in_b),
-        fp8_swap_out_s=statistics.median(out_f) if fp8 else None,
-        fp8_swap_in_s=statistics.median(in_f) if fp8 else None,
-        cold_pins=backend.pin_stats().get("host_pins", 0) - pins_at_start,
-    )
+            group = Fp8Layout.from_cache(cache).group_elems
+            if not round_trip_within_bound(before, after, group, ignore_nonfinite=True):
+                raise RuntimeError("KV values left the FP8 error bound across the swap round trip")
+        elif not torch.equal(before.view(torch.int16), after.view(torch.int16)):
+            raise RuntimeError("KV bytes changed across the swap round trip")
+
+    def row(self, tokens: int) -> dict:
+        cache = PagedKVCache(self.cfg, -(-tokens // 16), self.device, fill=False)
+        times: dict[tuple[str, str], list[float]] = {(fmt, way): [] for fmt in ("bf16", "fp8") for way in ("out", "in")}
+        pins_before_kept = None
+        for draw in range(self.warmup + self.repeats):
+            kept = draw >= self.warmup
+            if kept and pins_before_kept is None:
+                pins_before_kept = self.backend.pin_stats().get("host_pins", 0)
+            generator = torch.Generator(device=self.device).manual_seed(self.seed + draw)
+            cache.pool.copy_(torch.randn(cache.pool.shape, generator=generator, device=self.device, dtype=torch.float32))
+            for fmt in ("bf16", "fp8") if self.with_fp8 else ("bf16",):
+                sink_out, sink_in = (times[fmt, "out"], times[fmt, "in"]) if kept else ([], [])
+                self._round_trip(cache, fmt == "fp8", draw, sink_out, sink_in)
+        median = lambda key: statistics.median(times[key]) if times[key] else None  # noqa: E731
+        blocks = cache.allocator.num_blocks
+        return {
+            "tokens": tokens,
+            "blocks": blocks,
+            "bf16_bytes": blocks * cache.block_bytes,
+            "fp8_bytes": blocks * Fp8Layout.from_cache(cache).record_bytes,
+            "swap_out_s": median(("bf16", "out")),
+            "swap_in_s": median(("bf16", "in")),
+            "fp8_swap_out_s": median(("fp8", "out")),
+            "fp8_swap_in_s": median(("fp8", "in")),
+            "cold_pins": self.backend.pin_stats().get("host_pins", 0) - (pins_before_kept or 0),
+        }
 
 
-def describe(rows: list[Row], args: argparse.Namespace, device: torch.device, backend: NativeBackend, complete: bool) -> dict:
-    x = np.array([r.tokens for r in rows])
-    fits = {
-        "swap_out_s_coef": fit_nonnegative(x, np.array([r.swap_out_s for r in rows]), 1),
-        "swap_in_s_coef": fit_nonnegative(x, np.array([r.swap_in_s for r in rows]), 1),
-    }
-    if args.offload_dtype == "fp8":
-        fits["fp8_swap_out_s_coef"] = fit_nonnegative(x, np.array([r.fp8_swap_out_s for r in rows]), 1)
-        fits["fp8_swap_in_s_coef"] = fit_nonnegative(x, np.array([r.fp8_swap_in_s for r in rows]), 1)
+def summary(rows: list[dict], args: argparse.Namespace, device: torch.device, backend: NativeBackend, complete: bool) -> dict:
+    tokens = np.array([r["tokens"] for r in rows])
+    keys = SWAP_KEYS if args.offload_dtype == "fp8" else SWAP_KEYS[:2]
+    coefficients = {key: fit_nonnegative(tokens, np.array([r[key.removesuffix("_coef")] for r in rows]), 1) for key in keys}
     pins = backend.pin_stats()
+    on_gpu = device.type == "cuda"
     return {
         "model": args.model,
         "dtype": "bf16",
         "transfer": "native",
         "offload_dtype": args.offload_dtype,
-        "device": device.type,
-        "device_name": torch.cuda.get_device_name(device) if device.type == "cuda" else "cpu",
-        "measured_on_gpu": device.type == "cuda",
+        "device_name": torch.cuda.get_device_name(device) if on_gpu else "cpu",
+        "measured_on_gpu": on_gpu,
         "complete": complete,
         "staging_mib": args.staging_mib,
-        "repeats": args.repeats,
-        "warmup": args.warmup,
-        "cold_pins_in_kept_repeats": sum(r.cold_pins for r in rows),
-        "host_pins": pins.get("host_pins", 0),
-        "host_pin_gib": pins.get("host_pin_bytes", 0) / 2**30,
-        **fits,
-        "rows": [asdict(r) for r in rows],
+        "repeats_kept": args.repeats,
+        "repeats_discarded": args.warmup,
+        "host_pins_during_kept_repeats": sum(r["cold_pins"] for r in rows),
+        "host_pinned_gib": pins.get("host_pin_bytes", 0) / 2**30,
+        **coefficients,
+        "rows": rows,
     }
 
 
 def merge(swap: dict, cost_model: Path) -> dict:
-    """A reference cost model JSON with its swap coefficients replaced by these measurements;
-    recompute_s_coef and everything else of it kept."""
+    """A reference cost model JSON with its swap coefficients replaced by these measurements,
+    recompute_s_coef and everything else of it kept. A truncated sweep is refused, and a CPU
+    sweep never turns a GPU cost model into a GPU one."""
     if not swap["complete"]:
         raise ValueError("a truncated sweep is never merged into a cost model")
     merged = json.loads(cost_model.read_text())
-    for key in SWAP_KEYS:
-        if key in swap:
-            merged[key] = swap[key]
-    merged["transfer"] = "native"
-    merged["offload_dtype"] = swap["offload_dtype"]
-    merged["measured_on_gpu"] = bool(merged.get("measured_on_gpu")) and swap["measured_on_gpu"]
-    merged["swap_device_name"] = swap["device_name"]
+    merged.update({key: swap[key] for key in SWAP_KEYS if key in swap})
+    merged.update(transfer="native", offload_dtype=swap["offload_dtype"], swap_device_name=swap["device_name"],
+                  measured_on_gpu=bool(merged.get("measured_on_gpu")) and swap["measured_on_gpu"])
     return merged
 
 
 def parse_args(argv=None) -> argparse.Namespace:
-    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    p.add_argument("--model", default="qwen3_4b", choices=["qwen3_4b", "micro"])
-    p.add_argument("--device", default="cuda", choices=["cpu", "cuda"])
-    p.add_argument("--offload-dtype", default="fp8", choices=["bf16", "fp8"], help="also measure FP8 offload")
-    p.add_argument("--staging-mib", type=int, default=128)
-    p.add_argument("--host-cache-mib", type=int, default=8192)
-    p.add_argument("--tokens", type=int, nargs="+")
-    p.add_argument("--repeats", type=int, default=5)
-    p.add_argument("--warmup", type=int, default=1)
-    p.add_argument("--seed", type=int, default=0)
-    p.add_argument("--out", type=Path, default=Path("results/swap_costs"))
-    p.add_argument("--merge", type=Path, help="a cost_model.json from the reference's kv_crossover to update")
-    return p.parse_args(argv)
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--model", default="qwen3_4b", choices=["qwen3_4b", "micro"])
+    parser.add_argument("--device", default="cuda", choices=["cpu", "cuda"])
+    parser.add_argument("--offload-dtype", default="fp8", choices=["bf16", "fp8"], help="fp8 also measures FP8 records")
+    parser.add_argument("--staging-mib", type=int, default=128)
+    parser.add_argument("--host-cache-mib", type=int, default=8192)
+    parser.add_argument("--tokens", type=int, nargs="+", default=DEFAULT_TOKENS)
+    parser.add_argument("--repeats", type=int, default=5, help="repeats kept (medians)")
+    parser.add_argument("--warmup", type=int, default=1, help="leading repeats discarded")
+    parser.add_argument("--seed", type=int, default=0)
+    parser.add_argument("--out", type=Path, default=Path("results/swap_costs"))
+    parser.add_argument("--merge", type=Path, help="a cost_model.json from the reference's kv_crossover to update")
+    return parser.parse_args(argv)
+
+
+def _write_rows(path: Path, rows: list[dict]) -> None:
+    with path.open("w", newline="") as f:
+        writer = csv.DictWriter(f, fieldnames=ROW_FIELDS)
+        writer.writeheader()
+        writer.writerows(rows)
 
 
 def main(argv=None) -> dict:
@@ -221,39 +194,37 @@ def main(argv=None) -> dict:
     if args.offload_dtype == "fp8" and device.type != "cuda":
         raise SystemExit("FP8 offload runs on the GPU kernels only")
     cfg = ModelConfig.qwen3_4b() if args.model == "qwen3_4b" else ModelConfig.micro()
-    tokens = args.tokens or DEFAULT_TOKENS
     backend = NativeBackend(device, staging_bytes=args.staging_mib << 20, host_cache_bytes=args.host_cache_mib << 20)
-    # First-use work (staging, streams, FP8 stages) is not what a copy costs.
-    idle = PagedKVCache(cfg, 1, device)
-    backend.prepare(idle, False)
-    if args.offload_dtype == "fp8":
-        backend.prepare(idle, True)
-    del idle
+    # Staging, streams and FP8 stages made ahead, so no timed copy pays for first use.
+    warm = PagedKVCache(cfg, 1, device)
+    for fp8 in (False, True) if args.offload_dtype == "fp8" else (False,):
+        backend.prepare(warm, fp8)
+    del warm
 
+    sweep = Sweep(cfg, backend, device, args.offload_dtype == "fp8", args.repeats, args.warmup, args.seed)
     args.out.mkdir(parents=True, exist_ok=True)
-    partial = args.out / "swap_costs.partial.json"
-    rows: list[Row] = []
-    for n in tokens:
-        rows.append(measure(cfg, n, backend, device, args.offload_dtype == "fp8", args.repeats, args.warmup, args.seed))
+    in_progress = args.out / "swap_costs.partial.json"
+    rows: list[dict] = []
+    for tokens in args.tokens:
+        rows.append(sweep.row(tokens))
         r = rows[-1]
-        fp8_text = f"  fp8 out {r.fp8_swap_out_s * 1e3:8.2f} ms in {r.fp8_swap_in_s * 1e3:8.2f} ms" if r.fp8_swap_out_s is not None else ""
-        print(f"{n:>6} tokens  {r.bf16_bytes / 2**30:7.3f} GiB  bf16 out {r.swap_out_s * 1e3:8.2f} ms in {r.swap_in_s * 1e3:8.2f} ms{fp8_text}", flush=True)
-        with (args.out / "swap_costs.csv").open("w", newline="") as f:
-            writer = csv.DictWriter(f, fieldnames=list(asdict(rows[0])))
-            writer.writeheader()
-            writer.writerows(asdict(row) for row in rows)
-        partial.write_text(json.dumps(describe(rows, args, device, backend, False), indent=2) + "\n")
-    meta = describe(rows, args, device, backend, True)
+        line = f"{tokens:>6} tokens  {r['bf16_bytes'] / 2**30:7.3f} GiB  bf16 out {r['swap_out_s'] * 1e3:8.2f} ms  in {r['swap_in_s'] * 1e3:8.2f} ms"
+        if r["fp8_swap_out_s"] is not None:
+            line += f"  fp8 out {r['fp8_swap_out_s'] * 1e3:8.2f} ms  in {r['fp8_swap_in_s'] * 1e3:8.2f} ms"
+        print(line, flush=True)
+        _write_rows(args.out / "swap_costs.csv", rows)
+        in_progress.write_text(json.dumps(summary(rows, args, device, backend, False), indent=2) + "\n")
+    result = summary(rows, args, device, backend, True)
     backend.close()
-    (args.out / "swap_costs.json").write_text(json.dumps(meta, indent=2) + "\n")
-    partial.unlink()
+    (args.out / "swap_costs.json").write_text(json.dumps(result, indent=2) + "\n")
+    in_progress.unlink()
     if args.merge is not None:
-        (args.out / "cost_model.json").write_text(json.dumps(merge(meta, args.merge), indent=2) + "\n")
-    if meta["cold_pins_in_kept_repeats"]:
-        print(f"WARNING: {meta['cold_pins_in_kept_repeats']} host pins inside kept repeats; raise --host-cache-mib", flush=True)
-    if not meta["measured_on_gpu"]:
-        print("WARNING: not a GPU measurement; do not use these numbers as results.")
-    return meta
+        (args.out / "cost_model.json").write_text(json.dumps(merge(result, args.merge), indent=2) + "\n")
+    if result["host_pins_during_kept_repeats"]:
+        print(f"note: {result['host_pins_during_kept_repeats']} host pins inside kept repeats; a larger --host-cache-mib avoids them")
+    if not result["measured_on_gpu"]:
+        print("note: a CPU sweep (host flavour), not a GPU measurement")
+    return result
 
 
 if __name__ == "__main__":
