@@ -617,9 +617,30 @@ namespace lt {
 
 using EngineTicket = SwapEngine<Device>::Ticket;
 
-// Runs one call on an engine and turns what it throws into a status: a Fault's own code,
-// anything else LT_ERR_DEVICE, after which the engine refuses all work (a device failure can
-// leave half a transfer enqueued).
+// The status of the exception being handled, its text kept in last_error: a Fault carries its
+// own code; a device back end's refusal of an argument (std::invalid_argument: a foreign pool,
+// a device index that does not exist) is LT_ERR_INVALID; anything else is LT_ERR_DEVICE.
+// Called only from inside a catch block.
+inline int status_of_current_exception() {
+    try {
+        throw;
+    } catch (const Fault& fault) {
+        last_error = fault.what();
+        return fault.code;
+    } catch (const std::invalid_argument& refusal) {
+        last_error = refusal.what();
+        return LT_ERR_INVALID;
+    } catch (const std::exception& failure) {
+        last_error = failure.what();
+        return LT_ERR_DEVICE;
+    } catch (...) {
+        last_error = "unknown failure";
+        return LT_ERR_DEVICE;
+    }
+}
+
+// Runs one call on an engine (its device made current first) and returns its status. After a
+// device failure the engine refuses all further work: one can leave half a transfer enqueued.
 template <class Call>
 int on_engine(lt_engine* engine, Call&& call) {
     if (engine == nullptr) {
@@ -630,17 +651,10 @@ int on_engine(lt_engine* engine, Call&& call) {
         engine->core.device().activate();
         call(engine->core);
         return LT_OK;
-    } catch (const Fault& fault) {
-        last_error = fault.what();
-        if (fault.code == LT_ERR_DEVICE) engine->core.poison();
-        return fault.code;
-    } catch (const std::invalid_argument& error) {  // a device back end's refusal (a foreign pool)
-        last_error = error.what();
-        return LT_ERR_INVALID;
-    } catch (const std::exception& error) {
-        last_error = error.what();
-        engine->core.poison();
-        return LT_ERR_DEVICE;
+    } catch (...) {
+        const int status = status_of_current_exception();
+        if (status == LT_ERR_DEVICE) engine->core.poison();
+        return status;
     }
 }
 
@@ -670,31 +684,26 @@ LT_EXPORT int lt_create(int device, uint64_t staging_bytes, uint32_t num_staging
     try {
         *out = new lt_engine(device, staging_bytes, num_staging, ids_capacity, host_cache_bytes);
         return LT_OK;
-    } catch (const lt::Fault& fault) {
-        lt::last_error = fault.what();
-        return fault.code;
-    } catch (const std::invalid_argument& error) {  // a device back end's refusal (bad index)
-        lt::last_error = error.what();
-        return LT_ERR_INVALID;
-    } catch (const std::exception& error) {
-        lt::last_error = error.what();
-        return LT_ERR_DEVICE;
+    } catch (...) {
+        return lt::status_of_current_exception();
     }
 }
 
+// Always frees the engine. Teardown goes on past a failure (the device cannot be made
+// current, a stream cannot be drained); the first failure is the one reported.
 LT_EXPORT int lt_destroy(lt_engine* engine) {
     if (engine == nullptr) return LT_OK;
-    std::string problem;
+    std::unique_ptr<lt_engine> owned(engine);
+    std::vector<std::string> failures;
     try {
-        engine->core.device().activate();
-    } catch (const std::exception& error) {
-        problem = error.what();
+        owned->core.device().activate();
+    } catch (const std::exception& failure) {
+        failures.emplace_back(failure.what());
     }
-    const std::string closing = engine->core.close();
-    delete engine;
-    if (problem.empty()) problem = closing;
-    if (problem.empty()) return LT_OK;
-    lt::last_error = problem;
+    if (std::string closing = owned->core.close(); !closing.empty()) failures.push_back(std::move(closing));
+    owned.reset();
+    if (failures.empty()) return LT_OK;
+    lt::last_error = failures.front();
     return LT_ERR_DEVICE;
 }
 
