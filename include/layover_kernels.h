@@ -86,8 +86,10 @@ typedef struct {
 } lk_decode_shape;
 
 /* Bytes of device workspace lk_paged_decode needs for this shape (split-K partial results).
- * Depends only on the shape, never on lengths, so it can be sized once per batch layout. Its
- * contents need no initialization. Calls that share a workspace must not overlap in time. */
+ * Depends only on the shape and on the current device's compute-unit count (a grid too small
+ * to fill the GPU gets about one workgroup per CU), never on lengths, so it can be sized once
+ * per batch layout. Its contents need no initialization. Calls that share a workspace must not
+ * overlap in time. */
 uint64_t lk_paged_decode_workspace(const lk_decode_shape* shape);
 
 /* One decode step of one layer: out[b, h] = softmax(q[b,h] . K^T * scale) V over the first
@@ -167,13 +169,14 @@ int lk_fp8_append(void* records, const int32_t* write_block, const int32_t* writ
 
 /* lk_kv_write (BF16 pool) or lk_fp8_append (FP8 records) of each row's new token into layer
  * shape->layer, then lk_paged_decode of that layer, as one decode launch where the shape
- * allows (the workgroups that read a row's last block write its token first). No counterpart
+ * allows (the wave that reads a row's last block for a KV head writes that head's token and
+ * uses the written values for that block without re-reading them). No counterpart
  * in the reference, whose decode step writes the pool and then attends (layover/model.py:
  * 139-141); for small-batch steps, which are bound by launches. The write position must be
  * the row's last token: write_block[b*write_stride] = table[b][(lengths[b] - 1) / slots] and
  * write_slot[b*write_stride] = (lengths[b] - 1) % slots, as PagedKVCache.decode_rows packs
  * them; it is not checked. Rows must name distinct blocks. On the fused path the token is
- * written by the workgroups that read the row's last block, so a row is written only when
+ * written by the waves that read the row's last block, so a row is written only when
  * 1 <= lengths[b] <= table_width * slots (the range lk_paged_decode accepts); a row outside it
  * is neither read nor written. Other shapes run the two launches. */
 int lk_paged_decode_append(const lk_decode_shape* shape, const void* q, void* pool, const int32_t* table, const int32_t* lengths,
