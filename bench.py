@@ -700,6 +700,74 @@ def decode_scan(device) -> list:
     return rows
 
 
+def duplex_bench(device, blocks: int = 2048, repeats: int = 3) -> list:
+    """One session swapping out while another swaps in (`--duplex`): two backends, one per
+    direction, on a 12 GiB Qwen3-4B pool, against the same two transfers one after the
+    other. Copies to the host run as runtime blit kernels, copies to the device on the DMA
+    engines, so PCIe can carry both directions at once when the streams involved (each
+    backend's copy stream and kernel or compute stream, plus torch's) get hardware queues of
+    their own; GPU_MAX_HW_QUEUES, as the process was started, is reported beside the result.
+    A sample of 64 restored blocks is checked against the swapped-out source bytes (BF16) or
+    against a quiet restore of the same payload (FP8). (The pool is never indexed with all
+    2,048 ids at once: torch's gather over that many 2.36 MB rows of a 12 GiB pool faulted.)"""
+    import numpy as np
+    import torch
+
+    from layover_amd.config import ModelConfig
+    from layover_amd.kernels.fp8 import Fp8Layout
+    from layover_amd.kv.paged_cache import PagedKVCache
+    from layover_amd.kv.transfer import NativeBackend
+
+    pool_blocks = (12 << 30) // 2_359_296
+    cache = PagedKVCache(ModelConfig.qwen3_4b(), pool_blocks, device=device, fill=False)
+    fill_pool(cache.pool, seed=0)
+    order = np.random.default_rng(1).permutation(pool_blocks)
+    leaving = [int(i) for i in order[:blocks]]
+    returning = [int(i) for i in order[blocks : 2 * blocks]]
+    sample = torch.tensor(returning[:: blocks // 64][:64], device=device)
+    outward = NativeBackend(device, staging_bytes=128 << 20, num_staging=2)
+    inward = NativeBackend(device, staging_bytes=128 << 20, num_staging=2)
+    rows = []
+    for fp8 in (True, False):
+        for backend in (outward, inward):
+            backend.prepare(cache, fp8)
+        stored = inward.start_out(cache, returning, fp8)  # the session to restore
+        stored.wait()
+        expected = cache.pool[sample].clone()
+        if fp8:  # what a restore of this payload writes, measured alone
+            inward.start_in(cache, returning, stored.payload).wait()
+            expected = cache.pool[sample].clone()
+        sequential, concurrent = [], []
+        for _ in range(repeats + 1):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            out = outward.start_out(cache, leaving, fp8)
+            out.wait()
+            inward.start_in(cache, returning, stored.payload).wait()
+            t1 = time.perf_counter()
+            outward.free(out.payload)
+            torch.cuda.synchronize()
+            t2 = time.perf_counter()
+            out = outward.start_out(cache, leaving, fp8)
+            restore = inward.start_in(cache, returning, stored.payload)
+            out.wait()
+            restore.wait()
+            t3 = time.perf_counter()
+            outward.free(out.payload)
+            sequential.append((t1 - t0) * 1e3)
+            concurrent.append((t3 - t2) * 1e3)
+        exact = bool(torch.equal(cache.pool[sample].view(torch.int16), expected.view(torch.int16)))
+        inward.free(stored.payload)
+        per_way = blocks * (Fp8Layout.from_cache(cache).record_bytes if fp8 else cache.block_bytes)
+        best_seq, best_con = min(sequential[1:]), min(concurrent[1:])
+        rows.append({"format": "fp8" if fp8 else "bf16", "blocks_each_way": blocks, "bytes_each_way": per_way,
+                     "sequential_ms": round(best_seq, 2), "concurrent_ms": round(best_con, 2),
+                     "concurrent_gbs_both_ways": round(2 * per_way / (best_con * 1e-3) / 1e9, 1), "restore_exact": exact})
+    outward.close()
+    inward.close()
+    return rows
+
+
 def host_cores() -> int:
     return len(os.sched_getaffinity(0))
 
@@ -824,6 +892,7 @@ def main() -> None:
     parser.add_argument("--skip-distinct", action="store_true")
     parser.add_argument("--skip-graphs", action="store_true", help="skip the HIP-graph decode steps (rocprofv3 --pmc cannot follow replays)")
     parser.add_argument("--decode-scan", action="store_true", help="run only the batch-1 decode scan over context lengths and print it")
+    parser.add_argument("--duplex", action="store_true", help="run only the concurrent swap-out + swap-in measurement and print it")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this KV data path has no multi-GPU step (--gpus {args.gpus} refused)", file=sys.stderr)
@@ -841,6 +910,10 @@ def main() -> None:
     torch.cuda.set_device(device)
     if args.decode_scan:
         print(json.dumps({"decode_scan": decode_scan(device)}), flush=True)
+        return
+    if args.duplex:
+        queues = os.environ.get("GPU_MAX_HW_QUEUES", "unset (HIP default 4)")
+        print(json.dumps({"swap_duplex": duplex_bench(device), "gpu_max_hw_queues": queues}), flush=True)
         return
     config = ModelConfig.qwen3_4b()
     block_bytes = 2 * config.num_hidden_layers * config.num_key_value_heads * 16 * config.head_dim * 2

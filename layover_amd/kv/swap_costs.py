@@ -83,20 +83,26 @@ class Sweep:
 
     def _round_trip(self, cache: PagedKVCache, fp8: bool, draw: int, outs: list[float], ins: list[float]) -> None:
         source, target = self._orders(cache.allocator.num_blocks, draw)
-        before = cache.pool[torch.tensor(source, device=self.device)]
+        before = self._rows(cache, source)
         with self._stopwatch(outs):
             offload = self.backend.start_out(cache, source, fp8)
             offload.wait()
         with self._stopwatch(ins):
             self.backend.start_in(cache, target, offload.payload).wait()
-        after = cache.pool[torch.tensor(target, device=self.device)]
+        after = self._rows(cache, target)
         self.backend.free(offload.payload)
-        if fp8:
-            group = Fp8Layout.from_cache(cache).group_elems
-            if not round_trip_within_bound(before, after, group, ignore_nonfinite=True):
+        group = Fp8Layout.from_cache(cache).group_elems
+        for old, new in zip(before, after):
+            if fp8 and not round_trip_within_bound(old, new, group, ignore_nonfinite=True):
                 raise RuntimeError("KV values left the FP8 error bound across the swap round trip")
-        elif not torch.equal(before.view(torch.int16), after.view(torch.int16)):
-            raise RuntimeError("KV bytes changed across the swap round trip")
+            if not fp8 and not torch.equal(old.view(torch.int16), new.view(torch.int16)):
+                raise RuntimeError("KV bytes changed across the swap round trip")
+
+    def _rows(self, cache: PagedKVCache, ids: list[int]) -> list[torch.Tensor]:
+        """The pool blocks `ids`, gathered 256 at a time: a single torch gather of a whole
+        32,768-token context (2,048 blocks, 2.4 G values) is more than its kernels should be
+        asked for in one call."""
+        return [cache.pool[torch.tensor(ids[i : i + 256], device=self.device)] for i in range(0, len(ids), 256)]
 
     def row(self, tokens: int) -> dict:
         cache = PagedKVCache(self.cfg, -(-tokens // 16), self.device, fill=False)
