@@ -122,9 +122,12 @@ def record_bytes(cache: PagedKVCache, fp8: bool) -> int:
 
 
 class PlainCopyBackend(TransferBackend):
-    """Whole-tensor copies through torch, finished when they return."""
+    """Copies through torch, finished when they return. BF16 blocks are gathered and scattered
+    at most `piece` blocks per torch call: one index kernel over thousands of 2.36 MB blocks
+    is more than it should be asked for (such a gather faulted on a 12 GiB pool)."""
 
     name = "plain"
+    piece = 256
 
     def start_out(self, cache: PagedKVCache, blocks: list[int], fp8: bool = False) -> Ticket:
         index = torch.tensor(blocks, dtype=torch.long, device=cache.device)
@@ -134,7 +137,10 @@ class PlainCopyBackend(TransferBackend):
             quantize_blocks(cache.pool, index.to(torch.int32), stage, layout)
             host = stage.cpu()
         else:
-            host = cache.pool.index_select(0, index).cpu().view(torch.uint8).reshape(-1)
+            host = torch.empty(len(blocks) * cache.block_bytes, dtype=torch.uint8)
+            for first in range(0, len(blocks), self.piece):
+                part = cache.pool.index_select(0, index[first : first + self.piece]).cpu().view(torch.uint8).reshape(-1)
+                host[first * cache.block_bytes : first * cache.block_bytes + part.numel()] = part
         return ReadyTicket(Payload(host, len(blocks), record_bytes(cache, fp8), fp8))
 
     def start_in(self, cache: PagedKVCache, blocks: list[int], payload: Payload) -> Ticket:
@@ -143,7 +149,9 @@ class PlainCopyBackend(TransferBackend):
         if payload.fp8:
             dequantize_blocks(records, index.to(torch.int32), cache.pool, Fp8Layout.from_cache(cache))
         else:
-            cache.pool.index_copy_(0, index, records.view(cache.pool.dtype).view(len(blocks), *cache.pool.shape[1:]))
+            rows = records.view(cache.pool.dtype).view(len(blocks), *cache.pool.shape[1:])
+            for first in range(0, len(blocks), self.piece):
+                cache.pool.index_copy_(0, index[first : first + self.piece], rows[first : first + self.piece])
         return ReadyTicket()
 
 
