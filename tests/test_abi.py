@@ -81,3 +81,18 @@ def test_fp8_append_refuses_bad_arguments_without_launching():
     assert b"layer" in kernels.lk_last_error()
     assert kernels.lk_fp8_append(ptr, ptr, ptr, 0, 1, ptr, ptr, 0, 36, 8, 16, 128, None) == _lib.LK_ERR_INVALID
     assert kernels.lk_fp8_append(ptr, ptr, ptr, 1, 1, ptr, ptr, 0, 36, 0, 16, 128, None) == _lib.LK_ERR_INVALID
+
+
+def test_headers_are_plain_c(tmp_path):
+    """Both headers compile as C99 with warnings as errors (the reference's bindings and any C
+    host include them), and every declared entry point is a function of that name."""
+    names = sorted(declared("layover_transfer.h") | declared("layover_kernels.h"))
+    source = tmp_path / "abi.c"
+    source.write_text(
+        "#include \"layover_transfer.h\"\n#include \"layover_kernels.h\"\n"
+        "typedef void (*entry)(void);\n"
+        "const entry entries[] = {\n" + "".join(f"    (entry){name},\n" for name in names) + "};\n"
+        "int main(void) { return entries[0] == 0; }\n")
+    result = subprocess.run(["gcc", "-std=c99", "-pedantic", "-Wall", "-Wextra", "-Werror", "-Wno-cast-function-type", "-fsyntax-only",
+                             f"-I{ROOT / 'include'}", str(source)], capture_output=True, text=True)
+    assert result.returncode == 0, result.stderr
