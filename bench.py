@@ -75,34 +75,28 @@ def fill_pool(pool, seed: int, outlier_fraction: float = 0.0) -> None:
         del values
 
 
-class KernelTimer:
-    """Wraps an FP8 kernel so each launch is bracketed by HIP events on the stream it is
-    launched on (the backend's own stream), for the kernel's average duration."""
+def time_launches(stream, launches, bytes_of_each) -> dict:
+    """Average duration of a run of kernel launches queued back to back on `stream`, timed by
+    one pair of HIP events recorded on that stream around the whole run (an event pair per
+    launch would add its own packets to every window). A bounded spin is queued first, so the
+    whole run is queued before the stream reaches it: a pause of the host thread cannot fall
+    inside the window."""
+    import torch
 
-    def __init__(self, kernel, bytes_of):
-        self.kernel = kernel
-        self.bytes_of = bytes_of
-        self.events = []
-        self.recording = False
-
-    def __call__(self, *args):
-        import torch
-
-        if not self.recording:
-            return self.kernel(*args)
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    total_bytes = sum(bytes_of_each)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        spin = getattr(torch.cuda, "_sleep", None)  # torch's test helper: a kernel that spins for n cycles
+        if spin is not None:
+            spin(200_000_000)
         start.record()
-        self.kernel(*args)
+        for launch in launches:
+            launch()
         end.record()
-        self.events.append((start, end, self.bytes_of(*args)))
-
-    def summary(self):
-        times = [s.elapsed_time(e) for s, e, _ in self.events]
-        total_bytes = sum(b for _, _, b in self.events)
-        launches = len(times)
-        mean_ms = sum(times) / launches
-        return {"launches": launches, "mean_ms": mean_ms, "bytes_per_launch": total_bytes / launches,
-                "achieved_gbs": total_bytes / (sum(times) * 1e-3) / 1e9}
+    end.synchronize()
+    ms = start.elapsed_time(end)
+    return {"launches": len(launches), "mean_ms": ms / len(launches), "bytes_per_launch": total_bytes / len(launches),
+            "achieved_gbs": total_bytes / (ms * 1e-3) / 1e9}
 
 
 def measure_link(device, nbytes: int = 512 << 20, repeats: int = 5) -> dict:
@@ -237,26 +231,19 @@ def swap_bench(args, device, pool_blocks: int, cache):
     # pace, so a kernel beside it measures the copy, not itself.
     log("swap: FP8 kernel leg")
     bytes_of = lambda ids: ids.shape[0] * (2 * layout.block_elems + layout.record_bytes)
-    quantize_timer = KernelTimer(quantize_blocks, lambda pool, ids, stage, lay: bytes_of(ids))
-    dequantize_timer = KernelTimer(lambda stage, ids, pool, lay: dequantize_blocks(stage, ids, pool, lay),
-                                   lambda stage, ids, pool, lay: bytes_of(ids))
     per = backend.engine.staging_bytes // layout.record_bytes
     segments = [(torch.tensor(src[i : i + per], dtype=torch.int32, device=device), torch.tensor(dst[i : i + per], dtype=torch.int32, device=device))
                 for i in range(0, len(src), per)]
     stages = backend.stages
-    quantize_timer.recording = dequantize_timer.recording = True
-    with torch.cuda.stream(backend.kernel_stream):
-        # A bounded spin first, so every launch and event below is queued before the stream
-        # reaches them: a pause of the host thread (one of 32 ms was seen) then cannot fall
-        # inside a launch's event window.
-        spin = getattr(torch.cuda, "_sleep", None)  # torch's test helper: a kernel that spins for n cycles
-        if spin is not None:
-            spin(200_000_000)
-        for _ in range(args.kernel_repeats):
-            for index, (out_ids, in_ids) in enumerate(segments):
-                stage = stages[index % len(stages)]
-                quantize_timer(cache.pool, out_ids, stage, layout)
-                dequantize_timer(stage, in_ids, cache.pool, layout)
+    quantize_runs, dequantize_runs, sizes = [], [], []
+    for _ in range(args.kernel_repeats):
+        for index, (out_ids, in_ids) in enumerate(segments):
+            stage = stages[index % len(stages)]
+            quantize_runs.append(lambda out_ids=out_ids, stage=stage: quantize_blocks(cache.pool, out_ids, stage, layout))
+            dequantize_runs.append(lambda in_ids=in_ids, stage=stage: dequantize_blocks(stage, in_ids, cache.pool, layout))
+            sizes.append(bytes_of(out_ids))
+    quantize = time_launches(backend.kernel_stream, quantize_runs, sizes)
+    dequantize = time_launches(backend.kernel_stream, dequantize_runs, sizes)
     torch.cuda.synchronize()
     backend.close()
     record_total = args.blocks * layout.record_bytes
@@ -266,8 +253,8 @@ def swap_bench(args, device, pool_blocks: int, cache):
         "in_ms": sorted(in_ms)[len(in_ms) // 2],
         "bytes_each_way": record_total,
         "bf16_bytes_each_way": args.blocks * cache.block_bytes,
-        "quantize": quantize_timer.summary(),
-        "dequantize": dequantize_timer.summary(),
+        "quantize": quantize,
+        "dequantize": dequantize,
         "parity_sample_records": len(sample),
         "segments_per_direction": math.ceil(args.blocks / ((args.staging_mib << 20) // layout.record_bytes)),
         "engine_memcpys": stats["memcpys"],
