@@ -268,7 +268,9 @@ __global__ __launch_bounds__(kWave* kWaves) __attribute__((amdgpu_waves_per_eu(K
     const int32_t* row_ids = a.table + uint64_t(seq) * a.table_stride + first;
     const uint32_t width_here = min(a.bps, a.table_width - first);
     const uint32_t listed = width_here > wave ? (width_here - wave + kDecodeWaves - 1) / kDecodeWaves : 0;
-    const int32_t listed_block = lane < listed ? row_ids[wave + lane * kDecodeWaves] : 0;
+    // Unconditional (lanes past the listed ones re-read the split's first id, which exists),
+    // so no branch stands between this load and the waits that follow it.
+    const int32_t listed_block = row_ids[lane < listed ? wave + lane * kDecodeWaves : 0];
     const int32_t length = a.lengths[uint64_t(seq) * a.lengths_stride];
 
     // B operands of QK: query head n (zero past the group), the dims kDimsOf(g, j) .. +8 that
@@ -426,19 +428,20 @@ __global__ __launch_bounds__(kWave* kWaves) __attribute__((amdgpu_waves_per_eu(K
 
     // The block ids (and FP8 shifts) of this wave's units, one unit per lane (at most 64:
     // blocks per split <= 256), held before any tile is loaded and read back with v_readlane,
-    // so no load inside the main loop has to wait for the tile loads issued ahead of it.
+    // so no load inside the main loop has to wait for the tile loads issued ahead of it. The
+    // shifts are loaded by every lane (block 0's past the wave's units) and read only when a
+    // unit is consumed, so the first tiles' loads go out without waiting for them: ids, then
+    // tiles and shifts together, two trips to memory before the first unit rather than three.
     const uint32_t mine = count > wave ? (count - wave + kDecodeWaves - 1) / kDecodeWaves : 0;
     const int32_t my_block = lane < mine ? listed_block : 0;
     int32_t my_k_shift = 0, my_v_shift = 0;
     if constexpr (KV == LK_FP8_RECORD) {
-        if (lane < mine) {
-            const int16_t* shifts = reinterpret_cast<const int16_t*>(a.pool + uint64_t(uint32_t(my_block)) * a.block_bytes + block_elems);
-            my_k_shift = shifts[head_tile];
-            my_v_shift = shifts[uint64_t(a.layers) * a.kv_heads + head_tile];
-        }
+        const int16_t* shifts = reinterpret_cast<const int16_t*>(a.pool + uint64_t(uint32_t(my_block)) * a.block_bytes + block_elems);
+        my_k_shift = shifts[head_tile];
+        my_v_shift = shifts[uint64_t(a.layers) * a.kv_heads + head_tile];
     }
 
-    auto fetch_block = [&](MfmaTile<KV>& tile, int32_t block, int32_t k_shift, int32_t v_shift) __attribute__((always_inline)) {
+    auto fetch_block = [&](MfmaTile<KV>& tile, int32_t block) __attribute__((always_inline)) {
         const uint8_t* base = a.pool + uint64_t(uint32_t(block)) * a.block_bytes;
         if constexpr (KV == LK_BF16) {
 #pragma unroll
@@ -466,13 +469,15 @@ __global__ __launch_bounds__(kWave* kWaves) __attribute__((amdgpu_waves_per_eu(K
                 tile.v[r][0] = w[0];
                 tile.v[r][1] = w[1];
             }
-            tile.k_shift = k_shift;
-            tile.v_shift = v_shift;
         }
     };
-    auto fetch = [&](MfmaTile<KV>& tile, uint32_t i) __attribute__((always_inline)) {
-        fetch_block(tile, __builtin_amdgcn_readlane(my_block, i), __builtin_amdgcn_readlane(my_k_shift, i),
-                    __builtin_amdgcn_readlane(my_v_shift, i));
+    auto fetch = [&](MfmaTile<KV>& tile, uint32_t i) __attribute__((always_inline)) { fetch_block(tile, __builtin_amdgcn_readlane(my_block, i)); };
+    // The shifts of the wave's unit i, taken when the unit is consumed.
+    auto shifts_of = [&](MfmaTile<KV>& tile, uint32_t i) __attribute__((always_inline)) {
+        if constexpr (KV == LK_FP8_RECORD) {
+            tile.k_shift = __builtin_amdgcn_readlane(my_k_shift, i);
+            tile.v_shift = __builtin_amdgcn_readlane(my_v_shift, i);
+        }
     };
 
     // Online-softmax state: lane (g, n) tracks head n over slots 4g..4g+3 of every unit (the
@@ -618,6 +623,7 @@ __global__ __launch_bounds__(kWave* kWaves) __attribute__((amdgpu_waves_per_eu(K
             for (int d = 0; d < kRing; ++d) {
                 if (i + d < mine) {
                     const uint32_t t = wave + (i + d) * kDecodeWaves;
+                    shifts_of(ring[d], i + d);
                     if (t == count - 1 && wave == writer) written(ring[d]);
                     consume(ring[d], t);
                 }
