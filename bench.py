@@ -49,7 +49,7 @@ HBM_PEAK_GBS = 8000.0
 # FETCH_SIZE counts half the bytes read by these kernels: lk_stream_probe's 8 GiB read shows
 # as 4 GiB, and its 4 GiB copy as 4 GiB of WRITE_SIZE. Per full 113-record launch:
 # 2 x 130,221 + 130,686 KiB measured against 390,636 KiB algorithmic.
-QUANTIZE_TRAFFIC_RATIO = 1.0012
+QUANTIZE_TRAFFIC_RATIO = 1.0026
 L4_FP8_SWAP_MS = 67.0  # the reference's published FP8 swap out+in at 8,192 tokens on an NVIDIA L4 (README.md:27, :115)
 QWEN = dict(layers=36, kv_heads=8, query_heads=32, slots=16, head_dim=128)
 POOL_BYTES = 12 << 30

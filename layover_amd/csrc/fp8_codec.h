@@ -25,6 +25,14 @@ namespace lk {
 
 constexpr uint32_t kWave = 64;
 constexpr uint32_t kCodecWaves = 4;  // waves per workgroup
+// Waves per workgroup of the Qwen-shaped record kernels (quantize_groups_2048,
+// dequantize_groups_2048), which give each wave one 2,048-value group. One: measured on MI355X
+// at the swap's 113-block launches, quantize 57.7-57.8 us per launch against 58.6-58.7 us with
+// four waves (59.3-59.8 with two); dequantize the same either way (62.1-62.4 us).
+#ifndef LK_RECORD_WAVES
+#define LK_RECORD_WAVES 1
+#endif
+constexpr uint32_t kRecordWaves = LK_RECORD_WAVES;
 
 // fp8.py:95-116: BF16 bits / 2**shift -> E4M3 byte, rounding the significand to nearest even.
 __device__ __forceinline__ uint32_t encode_e4m3(uint32_t bits, int32_t shift) {

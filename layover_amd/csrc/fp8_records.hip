@@ -39,10 +39,10 @@ __device__ __forceinline__ float power_of_two(int32_t e) { return __uint_as_floa
 // This wave's contiguous run of groups [first, stop) out of `total`: consecutive groups of a
 // block share its id, and a wave's next group is the next 4 KiB of the same block.
 __device__ __forceinline__ bool wave_range(uint64_t total, uint64_t& first, uint64_t& stop) {
-    const uint64_t waves = uint64_t(gridDim.x) * kCodecWaves;
+    const uint64_t waves = uint64_t(gridDim.x) * kRecordWaves;
     // readfirstlane: the wave index is uniform, so group indices and block-id reads stay in
     // scalar registers and scalar loads, whose waits do not wait on the vector loads in flight.
-    const uint64_t wave = uint64_t(blockIdx.x) * kCodecWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const uint64_t wave = uint64_t(blockIdx.x) * kRecordWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const uint64_t per = (total + waves - 1) / waves;
     first = wave * per;
     stop = first + per < total ? first + per : total;
@@ -121,7 +121,7 @@ __device__ __forceinline__ void quantize_finish(uint8_t* __restrict__ stage, uin
     if (lane == 0) *reinterpret_cast<int16_t*>(out + block_elems + 2ull * g) = int16_t(shift);
 }
 
-__global__ __launch_bounds__(kWave* kCodecWaves) void quantize_groups_2048(const uint16_t* __restrict__ pool,
+__global__ __launch_bounds__(kWave* kRecordWaves) void quantize_groups_2048(const uint16_t* __restrict__ pool,
                                                                          const int32_t* __restrict__ ids, uint8_t* __restrict__ stage,
                                                                          uint32_t count, uint32_t groups_per_block) {
     const uint32_t lane = threadIdx.x % kWave;
@@ -223,7 +223,7 @@ __device__ __forceinline__ void dequantize_finish(uint16_t* __restrict__ pool, u
                     lane);
 }
 
-__global__ __launch_bounds__(kWave* kCodecWaves) void dequantize_groups_2048(const uint8_t* __restrict__ stage,
+__global__ __launch_bounds__(kWave* kRecordWaves) void dequantize_groups_2048(const uint8_t* __restrict__ stage,
                                                                            const int32_t* __restrict__ ids, uint16_t* __restrict__ pool,
                                                                            uint32_t count, uint32_t groups_per_block) {
     const uint32_t lane = threadIdx.x % kWave;
@@ -322,12 +322,12 @@ void launch_stage_history_2048(const uint8_t* records, const int32_t* ids, uint6
 
 void launch_quantize_2048(const uint16_t* pool, const int32_t* ids, uint8_t* stage, uint32_t count, uint32_t groups_per_block,
                           uint32_t grid, hipStream_t stream) {
-    hipLaunchKernelGGL(quantize_groups_2048, dim3(grid), dim3(kWave * kCodecWaves), 0, stream, pool, ids, stage, count, groups_per_block);
+    hipLaunchKernelGGL(quantize_groups_2048, dim3(grid), dim3(kWave * kRecordWaves), 0, stream, pool, ids, stage, count, groups_per_block);
 }
 
 void launch_dequantize_2048(const uint8_t* stage, const int32_t* ids, uint16_t* pool, uint32_t count, uint32_t groups_per_block,
                             uint32_t grid, hipStream_t stream) {
-    hipLaunchKernelGGL(dequantize_groups_2048, dim3(grid), dim3(kWave * kCodecWaves), 0, stream, stage, ids, pool, count, groups_per_block);
+    hipLaunchKernelGGL(dequantize_groups_2048, dim3(grid), dim3(kWave * kRecordWaves), 0, stream, stage, ids, pool, count, groups_per_block);
 }
 
 }  // namespace lk

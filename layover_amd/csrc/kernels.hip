@@ -64,7 +64,9 @@ uint32_t codec_grid(uint64_t groups) {
         const char* text = getenv("LAYOVER_CODEC_WG_PER_CU");
         return text ? uint32_t(strtoul(text, nullptr, 10)) : 0u;
     }();
-    const uint32_t full = grid_for_groups(groups);
+    const uint64_t workgroups = (groups + kRecordWaves - 1) / kRecordWaves;
+    require(workgroups <= 0x7FFFFFFFull, "too many groups for one launch");
+    const uint32_t full = uint32_t(workgroups);
     if (per_cu == 0) return full;
     static int units[64] = {};
     int device = 0;
