@@ -20,6 +20,7 @@ Also measured in the same run (extra keys of the JSON line):
               32,768-token context, beside gather + torch flash attention on the same GPU
   overlap     configs[4]: decode steps while 2,048 blocks swap out and back in
   decode_distinct  configs[2] on a ~78 GB pool whose rows share no block
+  decode_fp8_distinct  configs[3]'s batch 32 on FP8 records of that pool (the same rows)
   hbm_probe   lk_stream_probe read and copy rates and lk_stream_probe_mix at the FP8 kernels' read/write mixes: the measured HBM ceilings
   swap_bf16   the same 512 blocks swapped raw (gather kernel + DMA), byte-exact
   cpu_baseline  the oracle's C restatement of the FP8 swap arithmetic on all 512 blocks, in
@@ -341,8 +342,10 @@ def decode_tables(rng, batch: int, lengths, pool_blocks: int, distinct: bool):
     return table
 
 
-def decode_bench(device, pool, lengths, steps: int, warmup: int, seed: int, distinct: bool = False, kv_pool=None, probe: bool = True):
-    """Time 36 single-layer launches per step; bytes are the reference's unique accounting."""
+def decode_bench(device, pool, lengths, steps: int, warmup: int, seed: int, distinct: bool = False, kv_pool=None, probe: bool = True,
+                 pool_blocks: int | None = None):
+    """Time 36 single-layer launches per step; bytes are the reference's unique accounting.
+    `pool` (BF16) may be None when `kv_pool` (FP8 records) and `pool_blocks` are given."""
     import numpy as np
     import torch
 
@@ -350,7 +353,7 @@ def decode_bench(device, pool, lengths, steps: int, warmup: int, seed: int, dist
 
     rng = np.random.default_rng(seed)
     batch = len(lengths)
-    pool_blocks = pool.shape[0]
+    pool_blocks = pool.shape[0] if pool_blocks is None else pool_blocks
     table = torch.from_numpy(decode_tables(rng, batch, lengths, pool_blocks, distinct)).to(device)
     lens = torch.tensor(lengths, dtype=torch.int32, device=device)
     generator = torch.Generator(device=device).manual_seed(seed)
@@ -640,22 +643,37 @@ def overlap_bench(device, cache, pool_blocks: int, swap_blocks: int = 2048, stag
     }
 
 
-def distinct_decode(device, steps: int) -> dict:
+def distinct_decode(device, steps: int) -> tuple[dict, dict]:
     """The config-3 decode on a pool with one distinct block per table entry (about 80 GB),
-    so no block is read by two sequences: the sensitivity run for the 12 GiB pool's aliasing."""
+    so no block is read by two sequences: the sensitivity run for the 12 GiB pool's aliasing.
+    Then config 4's batch 32 on FP8 records of that pool (about 40 GB more), the same rows."""
     import numpy as np
     import torch
+
+    from layover_amd.kernels.fp8 import Fp8Layout, quantize_blocks
+    from layover_amd.kernels.hip_decode import Fp8KVPool
 
     rng = np.random.default_rng(2)
     lengths = [int(n) for n in rng.integers(1024, 32769, size=32)]
     blocks = sum(-(-n // 16) for n in lengths)
     pool = torch.empty(blocks, 2, QWEN["layers"], QWEN["kv_heads"], 16, QWEN["head_dim"], dtype=torch.bfloat16, device=device)
     fill_pool(pool, seed=5)
-    run = decode_bench(device, pool, lengths, steps, 1, seed=3, distinct=True)
-    run["pool_gb"] = round(pool.numel() * 2 / 1e9, 1)
+    rounded = lambda run: {k: (round(v, 4) if isinstance(v, float) else v) for k, v in run.items()}
+    bf16 = decode_bench(device, pool, lengths, steps, 1, seed=3, distinct=True)
+    bf16["pool_gb"] = round(pool.numel() * 2 / 1e9, 1)
+    layout = Fp8Layout(16 * QWEN["head_dim"], 2 * QWEN["layers"] * QWEN["kv_heads"])
+    records = torch.empty(blocks, layout.record_bytes, dtype=torch.uint8, device=device)
+    for first in range(0, blocks, 512):
+        ids = torch.arange(first, min(blocks, first + 512), dtype=torch.int32, device=device)
+        quantize_blocks(pool, ids, records[first:].reshape(-1), layout)
     del pool
     torch.cuda.empty_cache()
-    return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in run.items()}
+    fp8_pool = Fp8KVPool(records, QWEN["layers"], QWEN["kv_heads"], 16, QWEN["head_dim"])
+    fp8 = decode_bench(device, None, lengths, steps, 1, seed=3, distinct=True, kv_pool=fp8_pool, pool_blocks=blocks)
+    fp8["pool_gb"] = round(records.numel() / 1e9, 1)
+    del records, fp8_pool
+    torch.cuda.empty_cache()
+    return rounded(bf16), rounded(fp8)
 
 
 def decode_scan(device) -> list:
@@ -1013,7 +1031,7 @@ def main() -> None:
         result["overlap"] = overlap_bench(device, cache, pool_blocks)
     if not args.skip_decode and not args.skip_distinct:
         log("decode on distinct blocks (~80 GB pool)")
-        result["decode_distinct"] = distinct_decode(device, args.decode_steps)
+        result["decode_distinct"], result["decode_fp8_distinct"] = distinct_decode(device, args.decode_steps)
 
     # Last, so its 12 GiB of buffers come and go after everything timed above.
     log("HBM probe")
