@@ -4,6 +4,10 @@ Pool layout [block, kind, layer, kv_head, slot, dim], kind 0 = K and 1 = V
 (paged_cache.py:40-49): all layers of a block are contiguous, so a block moves as one range
 and its FP8 record's groups are (kind, layer, kv_head) in pool order. decode_rows builds the
 reference's decode table rows (paged_cache.py:154-169).
+
+A sequence's BlockTable lists its blocks in token order; blocks are reference counted by the
+allocator, so tables can share a prefix (fork) and a shared block is copied before it is
+written (make_writable, prepare_write), as in paged_cache.py:58-101.
 """
 
 from __future__ import annotations
@@ -68,6 +72,56 @@ class PagedKVCache:
     def blocks_for(self, tokens: int) -> int:
         return -(-tokens // self.block_tokens)
 
+    # -- a sequence's blocks (paged_cache.py:58-101) --
+
+    def ensure_capacity(self, table: BlockTable, tokens: int) -> None:
+        """Append newly allocated blocks until the table can hold `tokens` tokens."""
+        short = self.blocks_for(tokens) - len(table.blocks)
+        if short > 0:
+            table.blocks += self.allocator.alloc(short)
+
+    def make_writable(self, table: BlockTable, index: int) -> None:
+        """Copy-on-write for the table's block `index`: if another table also holds it, this
+        table gets a fresh block with the same contents and lets go of the shared one."""
+        shared = table.blocks[index]
+        if self.allocator.refcount(shared) < 2:
+            return
+        (private,) = self.allocator.alloc(1)
+        self.pool[private].copy_(self.pool[shared])
+        self.allocator.decref(shared)
+        table.blocks[index] = private
+
+    def prepare_write(self, table: BlockTable, start: int, end: int) -> None:
+        """Make tokens [start, end) writable: grow the table to hold them, give it private
+        copies of the blocks they fall in, and extend its length to `end` if shorter."""
+        self.ensure_capacity(table, end)
+        for index in range(start // self.block_tokens, self.blocks_for(end)):
+            self.make_writable(table, index)
+        table.num_tokens = max(table.num_tokens, end)
+
+    def fork(self, table: BlockTable, tokens: int | None = None) -> BlockTable:
+        """A new table sharing the blocks that hold the first `tokens` tokens (default all of
+        them); each shared block gains a reference."""
+        tokens = table.num_tokens if tokens is None else tokens
+        if tokens > table.num_tokens:
+            raise ValueError(f"cannot fork {tokens} tokens from a table of {table.num_tokens}")
+        prefix = table.blocks[: self.blocks_for(tokens)]
+        for block in prefix:
+            self.allocator.incref(block)
+        return BlockTable(list(prefix), tokens)
+
+    def truncate(self, table: BlockTable, tokens: int) -> None:
+        """Keep the first `tokens` tokens; blocks past them lose this table's reference."""
+        keep = self.blocks_for(tokens)
+        dropped, table.blocks = table.blocks[keep:], table.blocks[:keep]
+        for block in dropped:
+            self.allocator.decref(block)
+        table.num_tokens = min(table.num_tokens, tokens)
+
+    def release(self, table: BlockTable) -> None:
+        """Drop all of the table's blocks; it is left empty."""
+        self.truncate(table, 0)
+
     def _upload(self, values) -> torch.Tensor:
         """Host values to the pool's device as one copy. On a GPU it goes through pinned memory
         so that it is queued behind work already launched instead of waiting for it
@@ -112,6 +166,18 @@ class PagedKVCache:
         flat = picked.permute(1, 2, 0, 3, 4).reshape(2, kv_heads, -1, head_dim)[:, :, :end]
         return flat[KEY], flat[VALUE]
 
+    def write_range(self, table: BlockTable, layer: int, start: int, k: torch.Tensor, v: torch.Tensor) -> None:
+        """k and v, [kv_heads, count, head_dim], stored at tokens [start, start + count) of the
+        table (paged_cache.py:130-136); the table must have been through prepare_write."""
+        _, blocks, slots = self.chunk_locations(table, start, k.shape[1])
+        self.write_at(blocks, slots, layer, k, v)
+
+    def read_range(self, table: BlockTable, layer: int, end: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """K and V of the table's first `end` tokens, each [kv_heads, end, head_dim]
+        (paged_cache.py:138-141)."""
+        ids = self._upload(np.asarray(table.blocks[: self.blocks_for(end)], dtype=np.int64))
+        return self.read_blocks(ids, layer, end)
+
     def decode_rows(self, tables: list[BlockTable], width: int | None = None) -> torch.Tensor:
         """One packed int32 row per table (paged_cache.py:154-169): the block and slot of its
         last token (where this step writes), its length, then its blocks, padded to `width`
@@ -136,3 +202,9 @@ class PagedKVCache:
         """decode_rows on the device, as the views one decode step's layers take."""
         packed = self._upload(self.decode_rows(tables))
         return DecodeBatch(packed[:, 0].long(), packed[:, 1].long(), packed[:, 3:], packed[:, 2])
+
+    def block_table_tensor(self, tables: list[BlockTable]) -> tuple[torch.Tensor, torch.Tensor]:
+        """The decode batch's padded block table [batch, width] and lengths [batch]
+        (paged_cache.py:171-175)."""
+        batch = self.decode_batch(tables)
+        return batch.table, batch.lengths
