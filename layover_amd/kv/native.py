@@ -55,6 +55,9 @@ STAT_FIELDS = (
 class Stats(ctypes.Structure):
     _fields_ = [(field, ctypes.c_uint64) for field in STAT_FIELDS]
 
+    def as_dict(self) -> dict[str, int]:
+        return {field: int(getattr(self, field)) for field in STAT_FIELDS}
+
 
 HOST_KERNEL = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p)
 
@@ -229,7 +232,7 @@ class Engine:
     def stats(self) -> dict[str, int]:
         snapshot = Stats()
         self._call("lt_get_stats", ctypes.byref(snapshot))
-        return {field: getattr(snapshot, field) for field in STAT_FIELDS}
+        return snapshot.as_dict()
 
     def host_alloc(self, nbytes: int) -> int:
         return self._returning_pointer("lt_host_alloc", nbytes)

@@ -345,6 +345,57 @@ class NativeBackend(TransferBackend):
         handle = self.engine.in_scatter(cache.pool.data_ptr(), cache.block_bytes, blocks, payload.pointer)
         return _EngineTicket(self.engine, handle, None, [])
 
+    # -- the per-block baseline (transfer.py:435-473) --
+
+    def start_out_per_block(self, cache: PagedKVCache, blocks: list[int], fp8: bool = False) -> Ticket:
+        """start_out without staging: one copy per block (or, for FP8, one per record after
+        the whole quantize has run), the measured baseline of bench/transfer_gather.py."""
+        self._check(cache, blocks)
+        if self.flavor == "hip":
+            torch.cuda.current_stream(self.device).synchronize()
+        if not blocks:
+            return ReadyTicket(Payload(torch.empty(0, dtype=torch.uint8), 0, record_bytes(cache, fp8), fp8))
+        if not fp8:
+            payload = self._pinned_payload(len(blocks), cache.block_bytes, False)
+            handle = self.engine.out_per_block(cache.pool.data_ptr(), cache.block_bytes, blocks, payload.pointer)
+            return _EngineTicket(self.engine, handle, payload, [])
+        layout, stage, holds = self._whole_stage(cache, len(blocks))
+        ids = self._lane.upload(blocks, holds)
+        self._lane.run(lambda: self._quantize(cache.pool, ids, stage, layout), holds)
+        self._settle_lane()
+        payload = self._pinned_payload(len(blocks), layout.record_bytes, True)
+        handle = self.engine.out_per_block(stage.data_ptr(), layout.record_bytes, list(range(len(blocks))), payload.pointer)
+        return _EngineTicket(self.engine, handle, payload, holds)
+
+    def start_in_per_block(self, cache: PagedKVCache, blocks: list[int], payload: Payload) -> Ticket:
+        """start_in without staging: one copy per block, or for FP8 one per record into a
+        stage the size of the payload, then the whole dequantize."""
+        self._check(cache, blocks)
+        if not blocks:
+            return ReadyTicket()
+        if not payload.fp8:
+            handle = self.engine.in_per_block(cache.pool.data_ptr(), cache.block_bytes, blocks, payload.pointer)
+            return _EngineTicket(self.engine, handle, None, [])
+        layout, stage, holds = self._whole_stage(cache, len(blocks))
+        copies = self.engine.in_per_block(stage.data_ptr(), layout.record_bytes, list(range(len(blocks))), payload.pointer)
+        self.engine.wait(copies)
+        self.engine.release(copies)
+        ids = self._lane.upload(blocks, holds)
+        self._lane.run(lambda: self._dequantize(stage, ids, cache.pool, layout), holds)
+        return _EngineTicket(self.engine, self.engine.ext_finish(self._lane.handle), None, holds)
+
+    def _whole_stage(self, cache: PagedKVCache, count: int) -> tuple[Fp8Layout, torch.Tensor, list]:
+        layout = Fp8Layout.from_cache(cache)
+        self._fp8_ready(layout)
+        stage = torch.empty(count * layout.record_bytes, dtype=torch.uint8, device=self.device)
+        return layout, stage, [cache.pool, stage]
+
+    def _settle_lane(self) -> None:
+        """Wait on the host until the work queued on the kernel lane has run."""
+        handle = self.engine.ext_finish(self._lane.handle)
+        self.engine.wait(handle)
+        self.engine.release(handle)
+
     # -- FP8 --
 
     def _fp8_ready(self, layout: Fp8Layout) -> None:

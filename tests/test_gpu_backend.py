@@ -165,3 +165,33 @@ def test_qwen3_4b_blocks_past_4_gib_round_trip_in_both_formats():
         backend.close()
         del cache
         torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("fp8", [False, True], ids=["bf16", "fp8"])
+def test_per_block_baseline_equals_the_oracle(fp8):
+    """The per-block baseline (reference transfer.py:435-473) moves the same bytes as the
+    staged swap: payload equal to the oracle's, restore equal to the oracle's round trip."""
+    from layover_amd.kernels.fp8 import Fp8Layout
+    from layover_amd.kv.transfer import NativeBackend
+
+    print(f"per-block baseline fp8={fp8}", flush=True)
+    cache = qwen_cache(20, seed=16)
+    backend = NativeBackend("cuda", staging_bytes=3 * cache.block_bytes, ids_capacity=64)
+    try:
+        ids, targets = [17, 3, 11, 0, 8], [1, 2, 19, 5, 13]
+        source = pool_bits(cache, ids)
+        ticket = backend.start_out_per_block(cache, ids, fp8)
+        ticket.wait()
+        expected = expected_payload(cache, ids, fp8)
+        assert np.array_equal(payload_bytes(ticket), expected)
+        backend.start_in_per_block(cache, targets, ticket.payload).wait()
+        if fp8:
+            layout = Fp8Layout.from_cache(cache)
+            restored = np.zeros_like(source)
+            oracle.dequantize_records(expected, list(range(5)), restored, layout.group_elems, layout.groups_per_block)
+        else:
+            restored = source
+        assert np.array_equal(pool_bits(cache, targets), restored)
+        assert backend.engine.stats()["memcpys"] == 10
+    finally:
+        backend.close()

@@ -117,6 +117,38 @@ def test_fp8_orchestration_orders_kernels_against_copies(delay_us):
         backend.close()
 
 
+@pytest.mark.parametrize("delay_us", [0, 1500])
+def test_per_block_baseline_copies_once_per_block_or_record(delay_us):
+    """start_out_per_block / start_in_per_block (reference transfer.py:435-473): no staging,
+    one copy per block each way (BF16) or per record after the whole stand-in quantize (FP8),
+    and the same bytes as the staged path."""
+    cache = filled_cache(16, seed=4)
+    layout = Fp8Layout.from_cache(cache)
+    backend = NativeBackend("cpu", staging_bytes=2 * cache.block_bytes, ids_capacity=64, fp8_kernels=stand_in_codec(layout))
+    try:
+        backend.engine.set_copy_delay_us(delay_us)
+        out_ids, in_ids = [14, 2, 9, 0, 5], [1, 3, 4, 6, 7]
+        bf16 = backend.start_out_per_block(cache, out_ids)
+        bf16.wait()
+        assert bf16.payload.memory.numpy().tobytes() == block_bytes(cache, out_ids)
+        backend.start_in_per_block(cache, in_ids, bf16.payload).wait()
+        assert block_bytes(cache, in_ids) == block_bytes(cache, out_ids)
+        assert backend.engine.stats()["memcpys"] == 10 and backend.engine.stats()["kernels"] == 0
+
+        flat = cache.pool.view(torch.uint8).reshape(16, -1)
+        expected = b"".join(flat[i, : layout.record_bytes].numpy().tobytes() for i in out_ids)
+        records = backend.start_out_per_block(cache, out_ids, fp8=True)
+        records.wait()
+        assert records.payload.fp8 and records.payload.memory.numpy().tobytes() == expected
+        targets = [8, 10, 11, 12, 13]
+        backend.start_in_per_block(cache, targets, records.payload).wait()
+        assert b"".join(flat[i, : layout.record_bytes].numpy().tobytes() for i in targets) == expected
+        assert backend.engine.stats()["memcpys"] == 20
+        assert isinstance(backend.start_out_per_block(cache, []), ReadyTicket)
+    finally:
+        backend.close()
+
+
 def test_fp8_offload_is_not_done_while_the_copy_stream_is_held():
     cache = filled_cache(8)
     layout = Fp8Layout.from_cache(cache)
