@@ -76,6 +76,16 @@ def fill_pool(pool, seed: int, outlier_fraction: float = 0.0) -> None:
         del values
 
 
+def rotating_slots(device, slot_bytes: int, total_bytes: int = 1 << 30) -> list:
+    """Staging slots for back-to-back kernel legs, used in turn: together at least 1 GiB (four
+    times the 256 MB Infinity Cache), so a slot is long out of the cache when it comes round
+    again. Zeroed here, so every byte a launch reads is defined."""
+    import torch
+
+    count = max(2, -(-total_bytes // slot_bytes))
+    return [torch.zeros(slot_bytes, dtype=torch.uint8, device=device) for _ in range(count)]
+
+
 def time_launches(stream, launches, bytes_of_each) -> dict:
     """Average duration of a run of kernel launches queued back to back on `stream`, timed by
     one pair of HIP events recorded on that stream around the whole run (an event pair per
@@ -225,27 +235,30 @@ def swap_bench(args, device, pool_blocks: int, cache):
     elapsed = time.perf_counter() - start
     stats = backend.engine.stats()
 
-    # The kernels' own rates: the step's quantize and dequantize launches (the same segments,
-    # staging buffers and stream), repeated back to back with no copy to the host beside them.
-    # In the steps above a segment's quantize overlaps the previous segment's copy to the host,
-    # which the runtime runs as a kernel; that copy holds its CUs' path to memory at the link's
-    # pace, so a kernel beside it measures the copy, not itself.
+    # The kernels' own rates: the step's quantize and dequantize launches (the same segments
+    # and stream), repeated back to back with no copy to the host beside them. In the steps
+    # above a segment's quantize overlaps the previous segment's copy to the host, which the
+    # runtime runs as a kernel; that copy holds its CUs' path to memory at the link's pace, so a
+    # kernel beside it measures the copy, not itself. Successive launches rotate over staging
+    # slots worth 1 GiB, four times the Infinity Cache, so no launch finds the records another
+    # just wrote in the cache: both sides of every launch go to HBM.
     log("swap: FP8 kernel leg")
     bytes_of = lambda ids: ids.shape[0] * (2 * layout.block_elems + layout.record_bytes)
     per = backend.engine.staging_bytes // layout.record_bytes
     segments = [(torch.tensor(src[i : i + per], dtype=torch.int32, device=device), torch.tensor(dst[i : i + per], dtype=torch.int32, device=device))
                 for i in range(0, len(src), per)]
-    stages = backend.stages
+    stages = rotating_slots(device, backend.engine.staging_bytes)
     quantize_runs, dequantize_runs, sizes = [], [], []
-    for _ in range(args.kernel_repeats):
+    for repeat in range(args.kernel_repeats):
         for index, (out_ids, in_ids) in enumerate(segments):
-            stage = stages[index % len(stages)]
+            stage = stages[(repeat * len(segments) + index) % len(stages)]
             quantize_runs.append(lambda out_ids=out_ids, stage=stage: quantize_blocks(cache.pool, out_ids, stage, layout))
             dequantize_runs.append(lambda in_ids=in_ids, stage=stage: dequantize_blocks(stage, in_ids, cache.pool, layout))
             sizes.append(bytes_of(out_ids))
     quantize = time_launches(backend.kernel_stream, quantize_runs, sizes)
     dequantize = time_launches(backend.kernel_stream, dequantize_runs, sizes)
     torch.cuda.synchronize()
+    del stages
     backend.close()
     record_total = args.blocks * layout.record_bytes
     return {
@@ -309,6 +322,7 @@ def bf16_swap_bench(args, device, pool_blocks: int, cache) -> dict:
         stats = backend.engine.stats()
     finally:
         backend.close()
+    kernels = bf16_kernel_leg(args, device, cache, src, dst)
     each_way = args.blocks * cache.block_bytes
     total_ms = sum(out_ms) / len(out_ms) + sum(in_ms) / len(in_ms)
     return {
@@ -320,7 +334,41 @@ def bf16_swap_bench(args, device, pool_blocks: int, cache) -> dict:
         "kernels": stats["kernels"],
         "parity": "byte-exact: payload and restored blocks equal the source blocks, all 512",
         "reference_l4_ms": 109.0,
+        "kernel_leg": kernels,
     }
+
+
+def bf16_kernel_leg(args, device, cache, src, dst) -> dict:
+    """The BF16 swap's gather and scatter kernels alone (lk_gather_blocks / lk_scatter_blocks,
+    the kernels lt_out_gather / lt_in_scatter launch): the step's segments (56 blocks per
+    128 MiB slot, 9 x 56 + 8 for 512 blocks) repeated back to back on one stream over rotating
+    staging slots (rotating_slots), timed by time_launches. Bytes per block: read + write of
+    2,359,296 B. Inside the swap the same launches run between copies on a mostly idle GPU
+    and take longer (see the profile)."""
+    import torch
+
+    from layover_amd.kernels.blocks import gather_blocks, scatter_blocks
+
+    per_segment = (args.staging_mib << 20) // cache.block_bytes
+    slots = rotating_slots(device, per_segment * cache.block_bytes)
+    as_ids = lambda ids: torch.tensor(ids, dtype=torch.int32, device=device)
+    segments = [(as_ids(src[i : i + per_segment]), as_ids(dst[i : i + per_segment])) for i in range(0, len(src), per_segment)]
+    stream = torch.cuda.Stream(device=device)
+    result = {"segment_blocks": per_segment, "segments": len(segments), "staging_slots": len(slots)}
+    turns = [(o, i, slots[n % len(slots)]) for n, (o, i) in enumerate(segments * args.kernel_repeats)]
+    for name, run in (("gather", lambda out_ids, in_ids, slot: gather_blocks(cache.pool, out_ids, slot)),
+                      ("scatter", lambda out_ids, in_ids, slot: scatter_blocks(slot, in_ids, cache.pool))):
+        launches = [lambda o=o, i=i, slot=slot, run=run: run(o, i, slot) for o, i, slot in turns]
+        sizes = [2 * o.numel() * cache.block_bytes for o, _, _ in turns]
+        with torch.cuda.stream(stream):
+            launches[0]()
+        timed = time_launches(stream, launches, sizes)
+        result[name] = {"mean_launch_us": round(timed["mean_ms"] * 1e3, 2), "achieved_gbs": round(timed["achieved_gbs"], 1),
+                        "frac": round(timed["achieved_gbs"] / HBM_PEAK_GBS, 4), "launches": timed["launches"]}
+    torch.cuda.synchronize()
+    del slots
+    torch.cuda.empty_cache()
+    return result
 
 
 def decode_tables(rng, batch: int, lengths, pool_blocks: int, distinct: bool):

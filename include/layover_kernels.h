@@ -193,6 +193,17 @@ int lk_paged_decode_append(const lk_decode_shape* shape, const void* q, void* po
 int lk_paged_decode_static(const lk_decode_shape* shape, const void* q, const void* pool, const int32_t* table,
                            const int32_t* lengths, void* out, void* stream);
 
+/* Block gather and scatter between a paged pool and contiguous staging: the kernels behind
+ * lt_out_gather / lt_in_scatter (the counterpart of the reference's gather_kernel /
+ * scatter_kernel, native/transfer_cuda.cu:20-28, which its C ABI does not export), for callers
+ * that stage blocks themselves and for measuring the kernels alone. lk_gather_blocks copies
+ * pool block ids[i] to staging bytes [i * block_bytes, (i + 1) * block_bytes) for i < count;
+ * lk_scatter_blocks copies the other way. ids are device uint32; pool and staging are device
+ * memory, 8-byte aligned, and block_bytes a positive multiple of 8 (the transfer ABI's rules).
+ * Block ids are not checked against the pool's size. */
+int lk_gather_blocks(const void* pool, const uint32_t* ids, uint32_t count, uint64_t block_bytes, void* staging, void* stream);
+int lk_scatter_blocks(void* pool, const uint32_t* ids, uint32_t count, uint64_t block_bytes, const void* staging, void* stream);
+
 /* Measurement support, no reference counterpart: stream `bytes` (a multiple of 16, 16-byte
  * aligned) from `src`, copying to `dst`, or only reading when dst is null (then `sink`, one
  * device uint32, is written only if the data hash to a value chosen never to occur). This is

@@ -328,9 +328,10 @@ void launch_quantize_2048(const uint16_t* pool, const int32_t* ids, uint8_t* sta
 // The dequantize launch reserves LDS it does not use, 8 KiB per single-wave workgroup, which
 // caps it at 20 waves per CU (160 KiB of LDS): fewer of its reads and writes are in flight at
 // once, and HBM serves its 1:2 read/write mix faster. Measured on MI355X at the swap's
-// 113-record launches (A/B in one process, twice): 62.3-62.6 us uncapped, 60.6-60.8 us with
-// 8 KiB, 60.9 with 6.5 KiB (25 per CU), 61.8-61.9 with 9.4-10.9 KiB (15-17 per CU). The same
-// caps only slow the quantize (58.2 -> 59.5-75 us), whose mix is 2:1 the other way.
+// 113-record launches back to back, staging rotated over 1 GiB (A/B in one process): 62.9 us
+// uncapped, 61.0 us with 8 KiB. With the staging in two slots (partly cached): 62.3-62.6
+// uncapped, 60.6-60.8 with 8 KiB, 60.9 with 6.5 KiB (25 per CU), 61.8-61.9 with 9.4-10.9 KiB
+// (15-17 per CU). The same caps only slow the quantize (58.2 -> 59.5-75 us).
 constexpr uint32_t kDequantizeOccupancyLds = 8192;
 
 void launch_dequantize_2048(const uint8_t* stage, const int32_t* ids, uint16_t* pool, uint32_t count, uint32_t groups_per_block,

@@ -10,6 +10,7 @@
 #include <stdexcept>
 #include <string>
 
+#include "block_copy.h"
 #include "decode_attention.h"
 #include "prefill_attention.h"
 #include "fp8_codec.h"
@@ -858,6 +859,38 @@ LK_EXPORT int lk_paged_prefill_split(const lk_prefill_shape* shape, const void* 
     return lk::guarded([&] {
         lk::require(shape != nullptr, "null shape");
         lk::run_prefill(*shape, q, pool, block_ids, num_block_ids, out, workspace, workspace_bytes, true, static_cast<hipStream_t>(stream));
+    });
+}
+
+namespace lk {
+
+// The arguments lt_out_gather / lt_in_scatter accept, checked the same way.
+void check_block_copy(const void* pool, const uint32_t* ids, uint32_t count, uint64_t block_bytes, const void* staging) {
+    require(pool != nullptr && staging != nullptr && (ids != nullptr || count == 0), "null pool, ids or staging");
+    require(block_bytes > 0 && block_bytes % 8 == 0 && aligned(pool, 8) && aligned(staging, 8),
+            "pool and staging must be 8-byte aligned and block_bytes a positive multiple of 8");
+    require(blockcopy::chunks_for(block_bytes, false) * count <= 0x7FFFFFFFull, "too many chunks for one launch");
+}
+
+}  // namespace lk
+
+LK_EXPORT int lk_gather_blocks(const void* pool, const uint32_t* ids, uint32_t count, uint64_t block_bytes, void* staging, void* stream) {
+    return lk::guarded([&] {
+        lk::check_block_copy(pool, ids, count, block_bytes, staging);
+        if (count == 0) return;
+        const hipError_t status = blockcopy::launch_gather(static_cast<hipStream_t>(stream), static_cast<const uint8_t*>(pool), ids,
+                                                           static_cast<uint8_t*>(staging), block_bytes, count);
+        if (status != hipSuccess) throw std::runtime_error(std::string("gather_blocks launch failed: ") + hipGetErrorString(status));
+    });
+}
+
+LK_EXPORT int lk_scatter_blocks(void* pool, const uint32_t* ids, uint32_t count, uint64_t block_bytes, const void* staging, void* stream) {
+    return lk::guarded([&] {
+        lk::check_block_copy(pool, ids, count, block_bytes, staging);
+        if (count == 0) return;
+        const hipError_t status = blockcopy::launch_scatter(static_cast<hipStream_t>(stream), static_cast<uint8_t*>(pool), ids,
+                                                            static_cast<const uint8_t*>(staging), block_bytes, count);
+        if (status != hipSuccess) throw std::runtime_error(std::string("scatter_blocks launch failed: ") + hipGetErrorString(status));
     });
 }
 

@@ -1,6 +1,6 @@
 // The HIP flavour of include/layover_transfer.h for MI355X (gfx950). Replaces the reference's
 // native/transfer_cuda.cu: the swap engine (swap_engine.h) over HIP streams, events, copies to
-// and from pinned memory, and this file's gather and scatter kernels.
+// and from pinned memory, and the gather and scatter kernels of block_copy.h.
 //
 // Both directions of a copy are hipMemcpyAsync between device memory and pinned host memory.
 // Copies to the device run on an SDMA engine; copies to the host run as the runtime's blit
@@ -15,49 +15,10 @@
 #include <stdexcept>
 #include <string>
 
+#include "block_copy.h"
 #include "layover_transfer.h"
 
 namespace lt {
-
-// Block copy kernels. One workgroup of 256 lanes moves one 64 KiB chunk of one block:
-// grid.x = chunks_per_block * blocks, flattened, so there is no grid-y limit to respect.
-// Lane l moves words l, l + 256, ... of its chunk: each wave instruction touches 64
-// consecutive words (1 KiB with 16-byte words), which the memory system serves as whole
-// cache lines. 16-byte words when pool, staging and block_bytes allow it, else 8-byte words
-// (the ABI only promises 8-byte alignment).
-constexpr uint32_t kCopyLanes = 256;
-typedef uint32_t Word16 __attribute__((ext_vector_type(4)));
-typedef uint32_t Word8 __attribute__((ext_vector_type(2)));
-constexpr uint64_t kCopyChunk = 64 * 1024;
-
-template <class Word>
-__device__ __forceinline__ void copy_chunk(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, uint64_t bytes) {
-    const Word* from = reinterpret_cast<const Word*>(src);
-    Word* to = reinterpret_cast<Word*>(dst);
-    const uint32_t words = uint32_t(bytes / sizeof(Word));
-#pragma unroll 4
-    for (uint32_t w = threadIdx.x; w < words; w += kCopyLanes) to[w] = __builtin_nontemporal_load(from + w);
-}
-
-template <class Word>
-__global__ __launch_bounds__(kCopyLanes) void gather_blocks(const uint8_t* __restrict__ pool, const uint32_t* __restrict__ ids,
-                                                             uint8_t* __restrict__ staging, uint64_t block_bytes,
-                                                             uint32_t chunks_per_block) {
-    const uint32_t index = blockIdx.x / chunks_per_block;
-    const uint64_t offset = uint64_t(blockIdx.x % chunks_per_block) * kCopyChunk;
-    const uint64_t bytes = block_bytes - offset < kCopyChunk ? block_bytes - offset : kCopyChunk;
-    copy_chunk<Word>(pool + uint64_t(ids[index]) * block_bytes + offset, staging + uint64_t(index) * block_bytes + offset, bytes);
-}
-
-template <class Word>
-__global__ __launch_bounds__(kCopyLanes) void scatter_blocks(uint8_t* __restrict__ pool, const uint32_t* __restrict__ ids,
-                                                              const uint8_t* __restrict__ staging, uint64_t block_bytes,
-                                                              uint32_t chunks_per_block) {
-    const uint32_t index = blockIdx.x / chunks_per_block;
-    const uint64_t offset = uint64_t(blockIdx.x % chunks_per_block) * kCopyChunk;
-    const uint64_t bytes = block_bytes - offset < kCopyChunk ? block_bytes - offset : kCopyChunk;
-    copy_chunk<Word>(staging + uint64_t(index) * block_bytes + offset, pool + uint64_t(ids[index]) * block_bytes + offset, bytes);
-}
 
 class HipDevice {
    public:
@@ -151,32 +112,14 @@ class HipDevice {
     }
 
     void launch_gather(Stream stream, const uint8_t* pool, const uint32_t* ids, uint8_t* staging, uint64_t block_bytes, uint32_t blocks) {
-        const uint32_t chunks = chunks_for(block_bytes);
-        const dim3 grid(chunks * blocks);
-        if (wide(pool, staging, block_bytes))
-            hipLaunchKernelGGL(gather_blocks<Word16>, grid, dim3(kCopyLanes), 0, stream, pool, ids, staging, block_bytes, chunks);
-        else
-            hipLaunchKernelGGL(gather_blocks<Word8>, grid, dim3(kCopyLanes), 0, stream, pool, ids, staging, block_bytes, chunks);
-        check(hipGetLastError(), "launch gather_blocks");
+        check(blockcopy::launch_gather(stream, pool, ids, staging, block_bytes, blocks), "launch gather_blocks");
     }
 
     void launch_scatter(Stream stream, uint8_t* pool, const uint32_t* ids, const uint8_t* staging, uint64_t block_bytes, uint32_t blocks) {
-        const uint32_t chunks = chunks_for(block_bytes);
-        const dim3 grid(chunks * blocks);
-        if (wide(pool, staging, block_bytes))
-            hipLaunchKernelGGL(scatter_blocks<Word16>, grid, dim3(kCopyLanes), 0, stream, pool, ids, staging, block_bytes, chunks);
-        else
-            hipLaunchKernelGGL(scatter_blocks<Word8>, grid, dim3(kCopyLanes), 0, stream, pool, ids, staging, block_bytes, chunks);
-        check(hipGetLastError(), "launch scatter_blocks");
+        check(blockcopy::launch_scatter(stream, pool, ids, staging, block_bytes, blocks), "launch scatter_blocks");
     }
 
    private:
-    static uint32_t chunks_for(uint64_t block_bytes) { return uint32_t((block_bytes + kCopyChunk - 1) / kCopyChunk); }
-
-    static bool wide(const void* a, const void* b, uint64_t block_bytes) {
-        return ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) | block_bytes) & 15) == 0;
-    }
-
     static void check(hipError_t status, const char* call) {
         if (status != hipSuccess) throw std::runtime_error(std::string(call) + ": " + hipGetErrorName(status) + ": " + hipGetErrorString(status));
     }

@@ -71,6 +71,8 @@ SIGNATURES = {
     "lk_paged_decode_append": (c_int, [POINTER(DecodeShape), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_uint32, c_void_p,
                                        c_void_p, c_void_p, c_void_p, c_uint64, c_void_p]),
     "lk_paged_decode_static": (c_int, [POINTER(DecodeShape), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "lk_gather_blocks": (c_int, [c_void_p, c_void_p, c_uint32, c_uint64, c_void_p, c_void_p]),
+    "lk_scatter_blocks": (c_int, [c_void_p, c_void_p, c_uint32, c_uint64, c_void_p, c_void_p]),
     "lk_stream_probe": (c_int, [c_void_p, c_void_p, c_uint64, c_void_p, c_void_p]),
     "lk_stream_probe_mix": (c_int, [c_void_p, c_uint64, c_void_p, c_uint64, c_void_p]),
     "lk_tile_probe": (c_int, [POINTER(DecodeShape), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),

@@ -47,7 +47,7 @@ def test_kernel_library_exports_every_declared_symbol():
     assert names == {"lk_abi_version", "lk_last_error", "lk_fp8_quantize", "lk_fp8_dequantize", "lk_fp8_encode",
                      "lk_fp8_decode", "lk_paged_decode_workspace", "lk_paged_decode", "lk_stream_probe", "lk_fp8_append", "lk_kv_write",
                      "lk_paged_prefill", "lk_paged_prefill_workspace", "lk_paged_prefill_split", "lk_stream_probe_mix", "lk_paged_decode_append",
-                     "lk_paged_decode_static", "lk_tile_probe"}
+                     "lk_paged_decode_static", "lk_tile_probe", "lk_gather_blocks", "lk_scatter_blocks"}
     assert names <= exported(path)
     assert set(_lib.SIGNATURES) | {"lk_abi_version", "lk_last_error"} == names
 
@@ -81,6 +81,18 @@ def test_fp8_append_refuses_bad_arguments_without_launching():
     assert b"layer" in kernels.lk_last_error()
     assert kernels.lk_fp8_append(ptr, ptr, ptr, 0, 1, ptr, ptr, 0, 36, 8, 16, 128, None) == _lib.LK_ERR_INVALID
     assert kernels.lk_fp8_append(ptr, ptr, ptr, 1, 1, ptr, ptr, 0, 36, 0, 16, 128, None) == _lib.LK_ERR_INVALID
+
+
+def test_block_copies_refuse_bad_arguments_without_launching():
+    kernels = _lib.load()
+    word = ctypes.c_uint64(0)
+    ptr = ctypes.addressof(word)
+    assert kernels.lk_gather_blocks(None, ptr, 1, 64, ptr, None) == _lib.LK_ERR_INVALID
+    assert b"null" in kernels.lk_last_error()
+    assert kernels.lk_scatter_blocks(ptr, None, 1, 64, ptr, None) == _lib.LK_ERR_INVALID
+    assert kernels.lk_gather_blocks(ptr, ptr, 1, 12, ptr, None) == _lib.LK_ERR_INVALID
+    assert b"8-byte" in kernels.lk_last_error()
+    assert kernels.lk_scatter_blocks(ptr + 4, ptr, 1, 64, ptr, None) == _lib.LK_ERR_INVALID
 
 
 def test_headers_are_plain_c(tmp_path):
