@@ -134,8 +134,9 @@ def measure_link(device, nbytes: int = 512 << 20, repeats: int = 5) -> dict:
 
 
 def measure_hbm(device, nbytes: int = 8 << 30, repeats: int = 5) -> dict:
-    """HBM ceilings measured on this GPU with the library's streaming probes (each wave moves
-    one contiguous 4 KiB chunk once, non-temporal): read-only over 8 GiB, a copy of 4 GiB
+    """HBM ceilings measured on this GPU with the library's streaming probes (non-temporal; a
+    read moves 4 KiB per wave, a copy or mix 1 KiB per single-wave workgroup, the faster shape
+    for each): read-only over 8 GiB, a copy of 4 GiB
     (8 GiB of traffic), and the two traffic mixes of the FP8 record kernels: 8 GiB read and
     4 GiB written (quantize's 2:1), 4 GiB read and 8 GiB written (dequantize's 1:2). Reported
     beside the 8 TB/s specification; rates count bytes read plus bytes written."""

@@ -207,14 +207,17 @@ int lk_scatter_blocks(void* pool, const uint32_t* ids, uint32_t count, uint64_t 
 /* Measurement support, no reference counterpart: stream `bytes` (a multiple of 16, 16-byte
  * aligned) from `src`, copying to `dst`, or only reading when dst is null (then `sink`, one
  * device uint32, is written only if the data hash to a value chosen never to occur). This is
- * the HBM ceiling bench.py reports beside the 8 TB/s specification. */
+ * the HBM ceiling bench.py reports beside the 8 TB/s specification. Reads move 4 KiB per wave,
+ * copies 1 KiB per single-wave workgroup: the faster shape for each, measured on MI355X. */
 int lk_stream_probe(const void* src, void* dst, uint64_t bytes, uint32_t* sink, void* stream);
 
 /* Measurement support, no reference counterpart: the traffic mix of the FP8 record kernels.
- * Reads `src_bytes` from `src` and writes `dst_bytes` to `dst`, in the ratio 2:1 (as
- * lk_fp8_quantize: src_bytes a multiple of 4096) or 1:2 (as lk_fp8_dequantize: a multiple of
- * 2048), each wave moving one contiguous chunk of each. The measured ceiling for those kernels'
- * mix of reads and writes; LK_ERR_INVALID for any other ratio. */
+ * Reads `src_bytes` from `src` and writes `dst_bytes` to `dst` (both 16-byte aligned), in the
+ * ratio 2:1 (as lk_fp8_quantize: src_bytes a multiple of 16; output 8-byte word i is the two
+ * halves of input 16-byte word i XORed) or 1:2 (as lk_fp8_dequantize: src_bytes a multiple of
+ * 8; output 16-byte word i is input 8-byte word i twice), one single-wave workgroup per 64
+ * words. The measured ceiling for those kernels' mix of reads and writes; LK_ERR_INVALID for
+ * any other ratio. */
 int lk_stream_probe_mix(const void* src, uint64_t src_bytes, void* dst, uint64_t dst_bytes, void* stream);
 
 /* No counterpart in the reference; measurement only. Reads the K and V tiles that

@@ -273,6 +273,26 @@ __global__ __launch_bounds__(256) void stream_probe(const u32x4* __restrict__ sr
     }
 }
 
+// Streaming probes of one wave per workgroup: lane l of workgroup w reads input word
+// 64 w + l (16 or 8 bytes) and writes output word 64 w + l (16 or 8 bytes), non-temporally.
+// For mixed traffic this shape measured faster on MI355X than whole 4 KiB chunks per wave
+// (copy 6.7 against 6.1 TB/s, the 2:1 mix 6.9 against 6.2, the 1:2 mix 6.8 against 5.9).
+// kIn / kOut: bytes per word read / written; 16 / 8 XORs the input's halves, 8 / 16 repeats
+// the input word.
+template <int kIn, int kOut>
+__global__ __launch_bounds__(kWave) void wave_stream_probe(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, uint64_t words) {
+    const uint64_t word = uint64_t(blockIdx.x) * kWave + threadIdx.x;
+    if (word >= words) return;
+    if constexpr (kIn == 16) {
+        const u32x4 in = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src) + word);
+        if constexpr (kOut == 16) __builtin_nontemporal_store(in, reinterpret_cast<u32x4*>(dst) + word);
+        else __builtin_nontemporal_store(u32x2{in[0] ^ in[2], in[1] ^ in[3]}, reinterpret_cast<u32x2*>(dst) + word);
+    } else {
+        const u32x2 in = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(src) + word);
+        __builtin_nontemporal_store(u32x4{in[0], in[1], in[0], in[1]}, reinterpret_cast<u32x4*>(dst) + word);
+    }
+}
+
 // Tile probe: reads exactly the K and V tiles a decode launch of this shape reads from a BF16
 // pool (16 x 128 tiles, 4 KiB each) or an FP8-record pool (2 KiB tiles and the two groups'
 // shifts), in the decode kernel's order (KV head fastest, then the row's blocks, then the
@@ -903,8 +923,14 @@ LK_EXPORT int lk_stream_probe(const void* src, void* dst, uint64_t bytes, uint32
         lk::require(grid <= 0x7FFFFFFFull, "probe too large");
         const auto s = static_cast<hipStream_t>(stream);
         const auto in = static_cast<const lk::u32x4*>(src);
-        if (dst == nullptr) hipLaunchKernelGGL((lk::stream_probe<4, 0>), dim3(uint32_t(grid)), dim3(256), 0, s, in, nullptr, bytes / 16, sink);
-        else hipLaunchKernelGGL((lk::stream_probe<4, 4>), dim3(uint32_t(grid)), dim3(256), 0, s, in, static_cast<lk::u32x4*>(dst), bytes / 16, sink);
+        if (dst == nullptr) {
+            hipLaunchKernelGGL((lk::stream_probe<4, 0>), dim3(uint32_t(grid)), dim3(256), 0, s, in, nullptr, bytes / 16, sink);
+        } else {
+            const uint64_t words = bytes / 16, waves = (words + lk::kWave - 1) / lk::kWave;
+            lk::require(waves <= 0x7FFFFFFFull, "probe too large");
+            hipLaunchKernelGGL((lk::wave_stream_probe<16, 16>), dim3(uint32_t(waves)), dim3(lk::kWave), 0, s, static_cast<const uint8_t*>(src),
+                               static_cast<uint8_t*>(dst), words);
+        }
     });
 }
 
@@ -936,15 +962,15 @@ LK_EXPORT int lk_stream_probe_mix(const void* src, uint64_t src_bytes, void* dst
         lk::require(lk::aligned(src, 16) && lk::aligned(dst, 16), "16-byte alignment required");
         const bool two_to_one = src_bytes == 2 * dst_bytes, one_to_two = dst_bytes == 2 * src_bytes;
         lk::require(two_to_one || one_to_two, "src_bytes and dst_bytes must be in the ratio 2:1 or 1:2");
-        const uint64_t chunk = two_to_one ? 4096 : 2048;  // bytes read per wave
-        lk::require(src_bytes % chunk == 0, "src_bytes must be a multiple of 4096 (2:1) or 2048 (1:2)");
+        const uint64_t in_word = two_to_one ? 16 : 8;
+        lk::require(src_bytes % in_word == 0, "src_bytes must be a multiple of 16 (2:1) or 8 (1:2)");
         if (src_bytes == 0) return;
-        const uint64_t grid = (src_bytes / chunk + 3) / 4;
-        lk::require(grid <= 0x7FFFFFFFull, "probe too large");
+        const uint64_t words = src_bytes / in_word, waves = (words + lk::kWave - 1) / lk::kWave;
+        lk::require(waves <= 0x7FFFFFFFull, "probe too large");
         const auto s = static_cast<hipStream_t>(stream);
-        const auto in = static_cast<const lk::u32x4*>(src);
-        const auto out = static_cast<lk::u32x4*>(dst);
-        if (two_to_one) hipLaunchKernelGGL((lk::stream_probe<4, 2>), dim3(uint32_t(grid)), dim3(256), 0, s, in, out, src_bytes / 16, nullptr);
-        else hipLaunchKernelGGL((lk::stream_probe<2, 4>), dim3(uint32_t(grid)), dim3(256), 0, s, in, out, src_bytes / 16, nullptr);
+        const auto in = static_cast<const uint8_t*>(src);
+        const auto out = static_cast<uint8_t*>(dst);
+        if (two_to_one) hipLaunchKernelGGL((lk::wave_stream_probe<16, 8>), dim3(uint32_t(waves)), dim3(lk::kWave), 0, s, in, out, words);
+        else hipLaunchKernelGGL((lk::wave_stream_probe<8, 16>), dim3(uint32_t(waves)), dim3(lk::kWave), 0, s, in, out, words);
     });
 }

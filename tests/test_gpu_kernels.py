@@ -425,27 +425,26 @@ def test_stream_probe_reads_without_writing_and_copies_exactly(nbytes):
 
 @pytest.mark.parametrize("ratio", ["2:1", "1:2"])
 def test_stream_probe_mix_moves_the_stated_bytes(ratio):
-    """lk_stream_probe_mix: 2:1 writes, per 16-byte lane word k of a chunk's output, the XOR
-    of input words 2k and 2k + 1 of that lane; 1:2 writes input word k // 2. Nothing is written
-    past dst_bytes, and other ratios are refused."""
+    """lk_stream_probe_mix: 2:1 writes, as output 8-byte word i, the two halves of input
+    16-byte word i XORed; 1:2 writes input 8-byte word i twice as output 16-byte word i. A
+    partial last wave writes nothing past dst_bytes, and other ratios are refused."""
     from layover_amd.kernels import _lib
 
     lib = _lib.load()
     stream = _lib.current_stream(torch.device("cuda"))
-    chunks = 37
-    read_chunk = 4096 if ratio == "2:1" else 2048
-    src_bytes = chunks * read_chunk
+    words = 37 * 64 + 5
+    src_bytes = words * (16 if ratio == "2:1" else 8)
     dst_bytes = src_bytes // 2 if ratio == "2:1" else src_bytes * 2
     src = torch.randint(0, 2**31, (src_bytes // 4,), dtype=torch.int32, device="cuda")
     dst = torch.full((dst_bytes // 4 + 1024,), -7, dtype=torch.int32, device="cuda")
     _lib.check(lib.lk_stream_probe_mix(src.data_ptr(), src_bytes, dst.data_ptr(), dst_bytes, stream))
     torch.cuda.synchronize()
-    # [chunk, word k, lane, 4 dwords]
-    words_in = src.view(chunks, read_chunk // 1024, 64, 4).cpu()
     if ratio == "2:1":
-        expect = words_in[:, 0::2] ^ words_in[:, 1::2]
+        w = src.view(words, 4).cpu()
+        expect = torch.stack([w[:, 0] ^ w[:, 2], w[:, 1] ^ w[:, 3]], dim=1)
     else:
-        expect = words_in.repeat_interleave(2, dim=1)
+        w = src.view(words, 2).cpu()
+        expect = torch.cat([w, w], dim=1)
     assert torch.equal(dst[: dst_bytes // 4].cpu().view_as(expect), expect)
     assert bool((dst[dst_bytes // 4 :] == -7).all())
     with pytest.raises(_lib.KernelError):
