@@ -21,6 +21,8 @@ be given (`fp8_kernels`), because this package has no CPU codec.
 
 from __future__ import annotations
 
+import contextlib
+
 import ctypes
 from abc import ABC, abstractmethod
 from collections.abc import Callable
@@ -202,6 +204,7 @@ class _KernelLane:
         self._engine = engine
         self._device = device
         self._stream = torch.cuda.Stream(device=device) if engine.flavor == "hip" else None
+        self._entered = False
 
     @property
     def handle(self) -> int:
@@ -211,23 +214,35 @@ class _KernelLane:
     def stream(self):
         return self._stream
 
+    @contextlib.contextmanager
+    def active(self):
+        """Makes the lane torch's current stream for a whole transfer, so its uploads and
+        kernels are queued without switching streams once per launch (about 7 us each)."""
+        if self._stream is None or self._entered:
+            yield
+            return
+        with torch.cuda.stream(self._stream):
+            self._entered = True
+            try:
+                yield
+            finally:
+                self._entered = False
+
     def run(self, work: Callable[[], None], holds: list) -> None:
-        if self._stream is not None:
-            with torch.cuda.stream(self._stream):
-                work()
-        else:
+        if self._stream is None:
             holds.append(self._engine.host_call(self.handle, work))
+            return
+        with self.active():
+            work()
 
     def upload(self, blocks: list[int], holds: list) -> torch.Tensor:
         """The block ids as int32 on the device, copied from pinned memory in this lane's
         order (from pageable memory the copy would block the host until the stream drains)."""
-        ids = torch.tensor(blocks, dtype=torch.int32)
         if self._stream is None:
-            return ids
-        pinned = ids.pin_memory()
-        on_device = torch.empty(len(blocks), dtype=torch.int32, device=self._device)
-        with torch.cuda.stream(self._stream):
-            on_device.copy_(pinned, non_blocking=True)
+            return torch.tensor(blocks, dtype=torch.int32)
+        pinned = torch.tensor(blocks, dtype=torch.int32, pin_memory=True)
+        with self.active():
+            on_device = pinned.to(self._device, non_blocking=True)
         holds += [pinned, on_device]
         return on_device
 
@@ -423,6 +438,15 @@ class NativeBackend(TransferBackend):
         payload = self._pinned_payload(len(blocks), record, True) if out else restore_from
         lane, engine = self._lane, self.engine
         holds: list = [cache.pool]
+        with lane.active():
+            self._fp8_segments(cache, blocks, layout, payload, out, holds)
+        # Out ends with the last copy (copy stream); in ends with the last kernel (our lane).
+        handle = engine.ext_finish(None if out else lane.handle)
+        return _EngineTicket(engine, handle, payload if out else None, holds)
+
+    def _fp8_segments(self, cache: PagedKVCache, blocks: list[int], layout: Fp8Layout, payload: Payload, out: bool,
+                      holds: list) -> None:
+        lane, engine, record = self._lane, self.engine, layout.record_bytes
         ids = lane.upload(blocks, holds)
         for seg in self._segments(len(blocks), engine.staging_bytes // record):
             stage = self._stages[seg.slot]
@@ -439,9 +463,6 @@ class NativeBackend(TransferBackend):
                 engine.ext_wait(lane.handle, seg.slot, SLOT_FILLED)
                 lane.run(lambda stage=stage, seg_ids=seg_ids: self._dequantize(stage, seg_ids, cache.pool, layout), holds)
                 engine.ext_record(lane.handle, seg.slot, SLOT_RELEASED)
-        # Out ends with the last copy (copy stream); in ends with the last kernel (our lane).
-        handle = engine.ext_finish(None if out else lane.handle)
-        return _EngineTicket(engine, handle, payload if out else None, holds)
 
 
 def make_backend(name: str, device: torch.device | str = "cpu", **options) -> TransferBackend:
