@@ -116,12 +116,16 @@ def test_fp8_kernels_run_on_the_backends_stream_not_the_callers():
     backend = NativeBackend("cuda", staging_bytes=4 * cache.block_bytes, ids_capacity=64)
     try:
         backend.prepare(cache, fp8=True)
+        callers = torch.cuda.current_stream().cuda_stream
         ticket = backend.start_out(cache, [3, 1, 6], fp8=True)
+        assert torch.cuda.current_stream().cuda_stream == callers  # the lane is left on return
         ticket.wait()
         stream = backend.kernel_stream
         assert stream is not None
-        assert stream.cuda_stream != torch.cuda.current_stream().cuda_stream
+        assert stream.cuda_stream != callers
         assert np.array_equal(payload_bytes(ticket), expected_payload(cache, [3, 1, 6], True))
+        backend.start_in(cache, [2, 5, 7], ticket.payload).wait()
+        assert torch.cuda.current_stream().cuda_stream == callers
     finally:
         backend.close()
 
