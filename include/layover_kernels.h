@@ -200,7 +200,8 @@ int lk_paged_decode_static(const lk_decode_shape* shape, const void* q, const vo
  * pool block ids[i] to staging bytes [i * block_bytes, (i + 1) * block_bytes) for i < count;
  * lk_scatter_blocks copies the other way. ids are device uint32; pool and staging are device
  * memory, 8-byte aligned, and block_bytes a positive multiple of 8 (the transfer ABI's rules).
- * Block ids are not checked against the pool's size. */
+ * Block ids are not checked against the pool's size. count 0 copies nothing and accepts null
+ * pointers. */
 int lk_gather_blocks(const void* pool, const uint32_t* ids, uint32_t count, uint64_t block_bytes, void* staging, void* stream);
 int lk_scatter_blocks(void* pool, const uint32_t* ids, uint32_t count, uint64_t block_bytes, const void* staging, void* stream);
 

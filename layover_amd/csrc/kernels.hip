@@ -886,7 +886,7 @@ namespace lk {
 
 // The arguments lt_out_gather / lt_in_scatter accept, checked the same way.
 void check_block_copy(const void* pool, const uint32_t* ids, uint32_t count, uint64_t block_bytes, const void* staging) {
-    require(pool != nullptr && staging != nullptr && (ids != nullptr || count == 0), "null pool, ids or staging");
+    require(count == 0 || (pool != nullptr && staging != nullptr && ids != nullptr), "null pool, ids or staging");
     require(block_bytes > 0 && block_bytes % 8 == 0 && aligned(pool, 8) && aligned(staging, 8),
             "pool and staging must be 8-byte aligned and block_bytes a positive multiple of 8");
     require(blockcopy::chunks_for(block_bytes, false) * count <= 0x7FFFFFFFull, "too many chunks for one launch");

@@ -108,3 +108,4 @@ def test_headers_are_plain_c(tmp_path):
     result = subprocess.run(["gcc", "-std=c99", "-pedantic", "-Wall", "-Wextra", "-Werror", "-Wno-cast-function-type", "-fsyntax-only",
                              f"-I{ROOT / 'include'}", str(source)], capture_output=True, text=True)
     assert result.returncode == 0, result.stderr
+

@@ -6,6 +6,8 @@ equal to what the transfer engine's own staged gather delivers."""
 import numpy as np
 import pytest
 import torch
+from hypothesis import given, settings
+from hypothesis import strategies as st
 
 from oracle import oracle
 
@@ -83,3 +85,54 @@ def test_wrapper_refuses_what_the_kernels_cannot_take():
         gather_blocks(pool, torch.tensor([0, 1], dtype=torch.int64, device="cuda"), torch.empty(128, dtype=torch.uint8, device="cuda"))
     with pytest.raises(ValueError):
         gather_blocks(pool, torch.tensor([0, 1], dtype=torch.int32, device="cuda"), torch.empty(64, dtype=torch.uint8, device="cuda"))
+
+
+@settings(max_examples=50, deadline=None, derandomize=True)
+@given(
+    words=st.integers(1, 9000),
+    pool_blocks=st.integers(1, 24),
+    picks=st.lists(st.integers(0, 10**6), min_size=0, max_size=24),
+    pool_offset=st.sampled_from([0, 8]),
+    staging_offset=st.sampled_from([0, 8]),
+    seed=st.integers(0, 2**16),
+)
+def test_block_copies_over_drawn_sizes_counts_and_alignments(words, pool_blocks, picks, pool_offset, staging_offset, seed):
+    """Drawn cases: block sizes of 8 to 72,000 bytes (whole 1 KiB chunks or a ragged last one,
+    16- or only 8-byte aligned: both word widths), 0-24 blocks, gather ids that repeat, pool
+    and staging placed 0 or 8 bytes into their allocations. Bytes equal the oracle's gather
+    and scatter; the bytes before and after the copied ranges keep their sentinels."""
+    from layover_amd.kernels.blocks import gather_blocks, scatter_blocks
+
+    block_bytes = 8 * words
+    print(f"block copy case: {block_bytes} B x {len(picks)} of {pool_blocks}, offsets {pool_offset}/{staging_offset}", flush=True)
+    rng = np.random.default_rng(seed)
+    pool_total = torch.from_numpy(rng.integers(0, 256, pool_offset + pool_blocks * block_bytes + 64, dtype=np.uint8)).cuda()
+    pool = pool_total[pool_offset : pool_offset + pool_blocks * block_bytes].view(pool_blocks, block_bytes)
+    before = pool_total.cpu().numpy()
+    out_ids = [p % pool_blocks for p in picks]
+    staging_total = torch.full((staging_offset + len(out_ids) * block_bytes + 64,), 0xA5, dtype=torch.uint8, device="cuda")
+    staging = staging_total[staging_offset : staging_offset + len(out_ids) * block_bytes]
+
+    gather_blocks(pool, torch.tensor(out_ids, dtype=torch.int32, device="cuda"), staging)
+    got = staging_total.cpu().numpy()
+    expected = oracle.gather(before[pool_offset : pool_offset + pool_blocks * block_bytes], block_bytes, out_ids)
+    assert np.array_equal(got[staging_offset : staging_offset + expected.size], expected)
+    assert (got[:staging_offset] == 0xA5).all() and (got[staging_offset + expected.size :] == 0xA5).all()
+
+    # Scatter into distinct ids (two writers of one block would race), from the gathered bytes.
+    in_ids = [int(i) for i in rng.permutation(pool_blocks)[: min(len(out_ids), pool_blocks)]]
+    scatter_blocks(staging[: len(in_ids) * block_bytes], torch.tensor(in_ids, dtype=torch.int32, device="cuda"), pool)
+    reference = before.copy()
+    oracle.scatter(reference[pool_offset : pool_offset + pool_blocks * block_bytes], block_bytes, in_ids, expected[: len(in_ids) * block_bytes])
+    assert np.array_equal(pool_total.cpu().numpy(), reference)
+
+
+def test_block_copies_of_nothing_accept_null_pointers():
+    """count 0 is a no-op whatever the pointers (an empty torch tensor's data pointer is null);
+    a bad block size is still refused."""
+    from layover_amd.kernels import _lib
+
+    kernels = _lib.load()
+    assert kernels.lk_gather_blocks(None, None, 0, 64, None, None) == _lib.LK_OK
+    assert kernels.lk_scatter_blocks(None, None, 0, 64, None, None) == _lib.LK_OK
+    assert kernels.lk_gather_blocks(None, None, 0, 12, None, None) == _lib.LK_ERR_INVALID
