@@ -52,7 +52,8 @@ const char* lk_last_error(void);
  * little-endian int16 shift per group: record_bytes = block_elems + 2*groups_per_block. Each
  * group is divided by 2**shift, shift = (largest finite nonzero BF16 exponent) - 134, or 0
  * for a group without one, and rounded to nearest even; see fp8.py:1-31 for the special
- * values. Bytes of `stage` past count*record_bytes are untouched. */
+ * values. Bytes of `stage` past count*record_bytes are untouched. count 0 writes nothing and
+ * accepts null pointers. */
 int lk_fp8_quantize(const void* pool, const int32_t* ids, uint32_t count, void* stage, uint64_t group_elems,
                     uint32_t groups_per_block, void* stream);
 

@@ -83,7 +83,7 @@ uint32_t codec_grid(uint64_t groups) {
 
 void check_records(const void* pool, const int32_t* ids, uint32_t count, const void* stage, uint64_t group_elems,
                    uint32_t groups_per_block) {
-    require(pool != nullptr && stage != nullptr && (ids != nullptr || count == 0), "null pool, ids or stage");
+    require(count == 0 || (pool != nullptr && stage != nullptr && ids != nullptr), "null pool, ids or stage");
     require(group_elems > 0 && groups_per_block > 0, "group_elems and groups_per_block must be positive");
     require(aligned(pool, 2), "the BF16 pool must be 2-byte aligned");
 }

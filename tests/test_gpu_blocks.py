@@ -127,7 +127,7 @@ def test_block_copies_over_drawn_sizes_counts_and_alignments(words, pool_blocks,
     assert np.array_equal(pool_total.cpu().numpy(), reference)
 
 
-def test_block_copies_of_nothing_accept_null_pointers():
+def test_copies_and_record_kernels_of_nothing_accept_null_pointers():
     """count 0 is a no-op whatever the pointers (an empty torch tensor's data pointer is null);
     a bad block size is still refused."""
     from layover_amd.kernels import _lib
@@ -136,3 +136,5 @@ def test_block_copies_of_nothing_accept_null_pointers():
     assert kernels.lk_gather_blocks(None, None, 0, 64, None, None) == _lib.LK_OK
     assert kernels.lk_scatter_blocks(None, None, 0, 64, None, None) == _lib.LK_OK
     assert kernels.lk_gather_blocks(None, None, 0, 12, None, None) == _lib.LK_ERR_INVALID
+    assert kernels.lk_fp8_quantize(None, None, 0, None, 2048, 576, None) == _lib.LK_OK
+    assert kernels.lk_fp8_dequantize(None, None, 0, None, 2048, 576, None) == _lib.LK_OK
