@@ -111,7 +111,9 @@ int lk_paged_decode(const lk_decode_shape* shape, const void* q, const void* poo
  * head_dim]; query head h reads KV head h / (query_heads / kv_heads). The chunk's own K/V
  * must already be in the pool. Replaces the reference's gather + FlashAttention
  * (layover/model.py:69-98, prefill_attention). Supported: 16 slots x 128 dims, BF16 q, BF16
- * or FP8-record pools. */
+ * or FP8-record pools; q, out, the pool and every pool block 16-byte aligned (an FP8 record,
+ * 2 x layers x kv_heads groups of 2,050 bytes, is when layers x kv_heads is a multiple of 4).
+ * Anything else is refused with LK_ERR_INVALID. */
 typedef struct {
     uint32_t tokens;      /* query tokens in the chunk */
     uint32_t start;       /* position of the chunk's first token */

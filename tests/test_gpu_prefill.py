@@ -4,9 +4,13 @@ Tolerance: the north star's 2e-2 absolute / 1e-2 relative, plus a tighter check 
 error stays within BF16 rounding of the output and of the weights (P enters the matrix cores
 as BF16): |err| <= 2^-7 |x| + 4e-3."""
 
+import os
+
 import numpy as np
 import pytest
 import torch
+from hypothesis import given, settings
+from hypothesis import strategies as st
 
 from oracle import oracle
 
@@ -201,3 +205,55 @@ def test_split_keys_match_the_oracle(start, tokens, fp8, splits, monkeypatch):
     out = paged_prefill_attention_hip(q, pool, 1, torch.from_numpy(block_ids).cuda(), start, 4)
     torch.cuda.synchronize()
     assert_close(out, oracle.prefill_attention(q.float().cpu().numpy(), state, 1, block_ids, start, 4))
+
+
+@settings(max_examples=25, deadline=None, derandomize=True)
+@given(
+    seed=st.integers(0, 2**16),
+    start=st.integers(0, 1500),
+    tokens=st.integers(1, 96),
+    kv_heads=st.integers(1, 4),
+    gqa=st.integers(1, 5),
+    layers=st.integers(1, 3),
+    fp8=st.booleans(),
+    splits=st.sampled_from([None, "2", "5"]),
+)
+def test_prefill_over_drawn_chunks_matches_the_oracle(seed, start, tokens, kv_heads, gqa, layers, fp8, splits):
+    """Drawn chunks (start 0-1,500, 1-96 tokens, so chunks begin and end anywhere in a block),
+    1-4 KV heads at GQA 1-5, BF16 pools and FP8 records (refused, unaligned, unless layers x
+    KV heads is a multiple of 4), the split count chosen by the
+    library or forced to 2 or 5; shuffled block ids with spare blocks in the pool. The split
+    count is set in the environment around each draw (hypothesis runs every draw inside one
+    call of the test, so a fixture could not)."""
+    saved = os.environ.pop("LAYOVER_PREFILL_SPLITS", None)
+    if splits is not None:
+        os.environ["LAYOVER_PREFILL_SPLITS"] = splits
+    try:
+        drawn_prefill_case(seed, start, tokens, kv_heads, gqa, layers, fp8, splits)
+    finally:
+        os.environ.pop("LAYOVER_PREFILL_SPLITS", None)
+        if saved is not None:
+            os.environ["LAYOVER_PREFILL_SPLITS"] = saved
+
+
+def drawn_prefill_case(seed, start, tokens, kv_heads, gqa, layers, fp8, splits):
+    from layover_amd.kernels._lib import KernelError
+    from layover_amd.kernels.hip_prefill import paged_prefill_attention_hip
+
+    end = start + tokens
+    used = -(-end // 16)
+    blocks = used + 2
+    layer = seed % layers
+    pool, bits = make_pool(blocks, layers, kv_heads, seed=seed, fp8=fp8)
+    rng = np.random.default_rng(seed)
+    block_ids = rng.permutation(blocks)[:used].astype(np.int32)
+    q = (torch.randn(kv_heads * gqa, tokens, 128, generator=torch.Generator().manual_seed(seed)) * 2).to(torch.bfloat16).cuda()
+    print(f"prefill case start={start} tokens={tokens} kv={kv_heads} gqa={gqa} layers={layers} fp8={fp8} splits={splits}", flush=True)
+    if fp8 and (layers * kv_heads) % 4:
+        # Records of 2 x layers x kv_heads groups of 2,050 bytes are not 16-byte aligned.
+        with pytest.raises(KernelError, match="16-byte aligned"):
+            paged_prefill_attention_hip(q, pool, layer, torch.from_numpy(block_ids).cuda(), start, gqa)
+        return
+    out = paged_prefill_attention_hip(q, pool, layer, torch.from_numpy(block_ids).cuda(), start, gqa)
+    torch.cuda.synchronize()
+    assert_close(out, oracle.prefill_attention(q.float().cpu().numpy(), bits, layer, block_ids, start, gqa))
