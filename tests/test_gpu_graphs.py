@@ -11,6 +11,8 @@ decode_graphs.py behaviour; tolerance as the other decode tests)."""
 import numpy as np
 import pytest
 import torch
+from hypothesis import given, settings
+from hypothesis import strategies as st
 
 from oracle import oracle
 
@@ -436,3 +438,43 @@ def test_fused_write_on_other_shapes_runs_the_two_launches(fp8):
     else:
         assert torch.equal(fused_pool.view(torch.int16), split_pool.view(torch.int16))
     assert torch.equal(fused.view(torch.int16), separate.view(torch.int16))
+
+
+@settings(max_examples=40, deadline=None, derandomize=True)
+@given(
+    seed=st.integers(0, 2**16),
+    shape=st.one_of(
+        st.just(QWEN_LIKE),
+        st.builds(dict, layers=st.integers(1, 3), kv_heads=st.integers(1, 3), slots=st.sampled_from([1, 4, 7, 16]),
+                  head_dim=st.sampled_from([8, 24, 40, 128])),
+    ),
+    blocks=st.integers(1, 8),
+    rows=st.integers(1, 8),
+    gains=st.lists(st.sampled_from([2.0**-30, 2.0**-8, 1.0, 64.0, 2.0**40]), min_size=8, max_size=8),
+    specials=st.booleans(),
+)
+def test_fp8_append_over_drawn_layouts_and_gains_is_bit_exact(seed, shape, blocks, rows, gains, specials):
+    """Drawn record layouts (the Qwen3-4B one, which takes the wave-per-group kernel, or small
+    ones, which take the generic one), 1-8 rows writing distinct blocks at drawn slots and
+    layers, each row's token scaled by 2^-30 ... 2^40 against records of N(0, 1) values (so
+    writes raise, keep or sit far under their groups' shifts), and sometimes infinity, NaN and
+    subnormals in the token: records bit-exact against oracle.append_tokens."""
+    rows = min(rows, blocks)
+    records = random_records(blocks, **shape, seed=seed)
+    rng = np.random.default_rng(seed)
+    write_blocks = rng.permutation(blocks)[:rows].astype(np.int32)
+    write_slots = rng.integers(0, shape["slots"], rows).astype(np.int32)
+    layer = int(rng.integers(0, shape["layers"]))
+    scale = np.asarray(gains[:rows], dtype=np.float32).reshape(rows, 1, 1)
+    k = oracle.bf16_bits(rng.standard_normal((rows, shape["kv_heads"], shape["head_dim"]), dtype=np.float32) * scale)
+    v = oracle.bf16_bits(rng.standard_normal((rows, shape["kv_heads"], shape["head_dim"]), dtype=np.float32) / scale)
+    if specials:
+        k[0, 0, :3] = [0x7F80, 0xFFC0, 0x0001]
+        v[-1, -1, :2] = [0x8003, 0xFF80]
+    print(f"append case {shape} blocks {blocks} rows {rows} layer {layer} specials {specials}", flush=True)
+    pool = fp8_pool(records, **shape)
+    pool.write(torch.from_numpy(write_blocks).cuda(), torch.from_numpy(write_slots).cuda(), layer,
+               torch.from_numpy(k.view(np.int16)).cuda().view(torch.bfloat16), torch.from_numpy(v.view(np.int16)).cuda().view(torch.bfloat16))
+    expected = oracle.append_tokens(records, shape["layers"], shape["kv_heads"], shape["slots"], shape["head_dim"], write_blocks,
+                                    write_slots, layer, k, v)
+    assert np.array_equal(pool.records.cpu().numpy(), expected)
