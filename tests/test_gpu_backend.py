@@ -6,6 +6,8 @@ what the pool holds, restores against oracle.scatter / dequantize_records."""
 import numpy as np
 import pytest
 import torch
+from hypothesis import given, settings
+from hypothesis import strategies as st
 
 from oracle import oracle
 
@@ -197,5 +199,57 @@ def test_per_block_baseline_equals_the_oracle(fp8):
             restored = source
         assert np.array_equal(pool_bits(cache, targets), restored)
         assert backend.engine.stats()["memcpys"] == 10
+    finally:
+        backend.close()
+
+
+@settings(max_examples=30, deadline=None, derandomize=True)
+@given(
+    seed=st.integers(0, 2**16),
+    fp8=st.booleans(),
+    slot_blocks=st.integers(1, 5),
+    slack=st.floats(0.0, 0.99),
+    count=st.integers(1, 25),
+    num_staging=st.integers(2, 3),
+)
+def test_staged_swaps_over_drawn_staging_and_counts_equal_the_oracle(seed, fp8, slot_blocks, slack, count, num_staging):
+    """Drawn staging slots (1-5 records or blocks, plus a part of one more that no whole block
+    fits in) and 1-25 blocks out of the reference's micro shape, so transfers take one segment
+    or many with a ragged last one, through two or three slots; out ids may repeat. Payload
+    bytes equal the oracle's gather or records, and the restore into distinct ids equals the
+    oracle's scatter or dequantization."""
+    from layover_amd.config import ModelConfig
+    from layover_amd.kernels.fp8 import Fp8Layout
+    from layover_amd.kv.paged_cache import PagedKVCache
+    from layover_amd.kv.transfer import NativeBackend
+
+    cache = PagedKVCache(ModelConfig.micro(), 32, device="cuda", fill=False)
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    cache.pool.copy_((torch.randn(cache.pool.shape, generator=gen, device="cuda") * 4).to(torch.bfloat16))
+    unit = Fp8Layout.from_cache(cache).record_bytes if fp8 else cache.block_bytes
+    staging = slot_blocks * unit + int(slack * unit) // 8 * 8
+    rng = np.random.default_rng(seed)
+    out_ids = [int(i) for i in rng.integers(0, 32, count)]
+    in_ids = [int(i) for i in rng.permutation(32)[:count]]
+    print(f"staged swap case fp8={fp8} staging={staging} ({slot_blocks} per slot) x{num_staging} count={count}", flush=True)
+    backend = NativeBackend("cuda", staging_bytes=staging, num_staging=num_staging, ids_capacity=64)
+    try:
+        source = pool_bits(cache, out_ids)
+        ticket = backend.start_out(cache, out_ids, fp8)
+        ticket.wait()
+        expected = expected_payload(cache, out_ids, fp8)
+        assert np.array_equal(payload_bytes(ticket), expected)
+        before = pool_bits(cache)
+        backend.start_in(cache, in_ids, ticket.payload).wait()
+        reference = before.reshape(32, -1).copy()
+        if fp8:
+            layout = Fp8Layout.from_cache(cache)
+            restored = np.zeros_like(source)
+            oracle.dequantize_records(expected, list(range(count)), restored, layout.group_elems, layout.groups_per_block)
+            reference[in_ids] = restored.reshape(count, -1)
+        else:
+            reference[in_ids] = source.reshape(count, -1)
+        assert np.array_equal(pool_bits(cache).reshape(32, -1), reference)
+        backend.free(ticket.payload)
     finally:
         backend.close()
