@@ -111,9 +111,10 @@ int lk_paged_decode(const lk_decode_shape* shape, const void* q, const void* poo
  * head_dim]; query head h reads KV head h / (query_heads / kv_heads). The chunk's own K/V
  * must already be in the pool. Replaces the reference's gather + FlashAttention
  * (layover/model.py:69-98, prefill_attention). Supported: 16 slots x 128 dims, BF16 q, BF16
- * or FP8-record pools; q, out, the pool and every pool block 16-byte aligned (an FP8 record,
- * 2 x layers x kv_heads groups of 2,050 bytes, is when layers x kv_heads is a multiple of 4).
- * Anything else is refused with LK_ERR_INVALID. */
+ * or FP8-record pools. q and out 16-byte aligned; a pool read in place 16-byte aligned, its
+ * blocks too. An FP8 record (2 x layers x kv_heads groups of 2,050 bytes) is aligned when
+ * layers x kv_heads is a multiple of 4; lk_paged_prefill_split stages records of other
+ * layouts as BF16 (they need only be 2-byte aligned), lk_paged_prefill refuses them. */
 typedef struct {
     uint32_t tokens;      /* query tokens in the chunk */
     uint32_t start;       /* position of the chunk's first token */

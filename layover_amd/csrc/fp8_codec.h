@@ -213,7 +213,8 @@ void launch_append_2048(uint8_t* records, const int32_t* write_block, const int3
                         hipStream_t stream);
 // One layer of the FP8 records of blocks ids[0 .. blocks) decoded into a compact one-layer BF16
 // pool `stage` [blocks][2][kv_heads][16 x 128], with index[b] = b (the paged prefill's
-// FP8 path). Groups of 2,048 values; the records' shifts follow their codes.
+// FP8 path). Groups of 2,048 values; the records' shifts follow their codes. records and
+// record_bytes need only be even.
 void launch_stage_history_2048(const uint8_t* records, const int32_t* ids, uint64_t record_bytes, uint32_t groups_per_block, uint32_t layer,
                                uint32_t layers, uint32_t kv_heads, uint32_t blocks, uint16_t* stage, int32_t* index, hipStream_t stream);
 

@@ -252,7 +252,10 @@ __global__ __launch_bounds__(kWave* kRecordWaves) void dequantize_groups_2048(co
 // group (block b, kind, KV head) = (w / (2 kv_heads), w / kv_heads % 2, w % kv_heads) of
 // block ids[b], and writes it to stage[b][kind][head] (16 x 128 BF16, a one-layer pool block);
 // the first wave of each block also writes index[b] = b. Same decode, bit for bit, as
-// dequantize_groups_2048.
+// dequantize_groups_2048. kWide: the records are 8-byte aligned and the codes are read 8 bytes
+// a lane; otherwise (records of a layout whose size is not a multiple of 8, always even) the
+// same bytes are read 2 at a time.
+template <bool kWide>
 __global__ __launch_bounds__(kWave* kCodecWaves) void stage_history_2048(const uint8_t* __restrict__ records,
                                                                        const int32_t* __restrict__ ids, uint64_t record_bytes,
                                                                        uint32_t groups_per_block, uint32_t layer, uint32_t layers,
@@ -265,10 +268,19 @@ __global__ __launch_bounds__(kWave* kCodecWaves) void stage_history_2048(const u
     const uint32_t kind = uint32_t(unit / kv_heads % 2), head = uint32_t(unit % kv_heads);
     const uint8_t* record = records + uint64_t(uint32_t(ids[b])) * record_bytes;
     const uint64_t group = (uint64_t(kind) * layers + layer) * kv_heads + head;
-    const u32x2* codes = reinterpret_cast<const u32x2*>(record + group * kFastGroup);
     u32x2 bytes[4];
+    if constexpr (kWide) {
+        const u32x2* codes = reinterpret_cast<const u32x2*>(record + group * kFastGroup);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) bytes[j] = __builtin_nontemporal_load(codes + j * kWave + lane);
+        for (int j = 0; j < 4; ++j) bytes[j] = __builtin_nontemporal_load(codes + j * kWave + lane);
+    } else {
+        const uint16_t* codes = reinterpret_cast<const uint16_t*>(record + group * kFastGroup);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint16_t* word = codes + 4 * (j * kWave + lane);
+            bytes[j] = u32x2{uint32_t(word[0]) | uint32_t(word[1]) << 16, uint32_t(word[2]) | uint32_t(word[3]) << 16};
+        }
+    }
     const int32_t shift = reinterpret_cast<const int16_t*>(record + uint64_t(kFastGroup) * groups_per_block)[group];
     decode_group_to<false>(reinterpret_cast<u32x4*>(stage + unit * kFastGroup), shift, bytes, lane);
     if (unit % (2 * kv_heads) == 0 && lane == 0) index[b] = int32_t(b);
@@ -316,8 +328,12 @@ void launch_stage_history_2048(const uint8_t* records, const int32_t* ids, uint6
                                uint32_t layers, uint32_t kv_heads, uint32_t blocks, uint16_t* stage, int32_t* index, hipStream_t stream) {
     const uint64_t waves = uint64_t(blocks) * 2 * kv_heads;
     const uint32_t grid = uint32_t((waves + kCodecWaves - 1) / kCodecWaves);
-    hipLaunchKernelGGL(stage_history_2048, dim3(grid), dim3(kWave * kCodecWaves), 0, stream, records, ids, record_bytes, groups_per_block, layer,
-                       layers, kv_heads, blocks, stage, index);
+    if (((reinterpret_cast<uintptr_t>(records) | record_bytes) & 7) == 0)
+        hipLaunchKernelGGL(stage_history_2048<true>, dim3(grid), dim3(kWave * kCodecWaves), 0, stream, records, ids, record_bytes, groups_per_block,
+                           layer, layers, kv_heads, blocks, stage, index);
+    else
+        hipLaunchKernelGGL(stage_history_2048<false>, dim3(grid), dim3(kWave * kCodecWaves), 0, stream, records, ids, record_bytes, groups_per_block,
+                           layer, layers, kv_heads, blocks, stage, index);
 }
 
 void launch_quantize_2048(const uint16_t* pool, const int32_t* ids, uint8_t* stage, uint32_t count, uint32_t groups_per_block,

@@ -708,8 +708,12 @@ PrefillPlan prefill_plan(const lk_prefill_shape& s) {
     const uint64_t rows = uint64_t(s.tokens) * groups;
     // The LDS-shared kernel (128 rows a workgroup) unless LAYOVER_PREFILL_KERNEL=1 asks for the
     // register-only one (64 rows a workgroup, each wave streaming its own tiles).
+    // FP8 records that are not 16-byte aligned (2 x layers x kv_heads groups of 2,050 bytes:
+    // layers x kv_heads not a multiple of 4) are always staged as BF16 for the LDS kernel,
+    // the only path that does not read the records in place.
+    const bool unaligned_records = s.kv_format == LK_FP8_RECORD && (uint64_t(2) * s.layers * s.kv_heads * (kDim * kSlots + 2)) % 16 != 0;
     const char* choice = getenv("LAYOVER_PREFILL_KERNEL");
-    p.shared = !(choice && strtoul(choice, nullptr, 10) == 1);
+    p.shared = unaligned_records || !(choice && strtoul(choice, nullptr, 10) == 1);
     const uint64_t tile_rows = p.shared ? uint64_t(kLdsRows) * kLdsWaves : uint64_t(kPrefillRows) * kPrefillWaves;
     p.row_tiles = (rows + tile_rows - 1) / tile_rows;
     const uint64_t end = uint64_t(s.start) + s.tokens;
@@ -718,7 +722,7 @@ PrefillPlan prefill_plan(const lk_prefill_shape& s) {
     p.split_steps = max_steps;
     if (!p.shared) return p;
     const char* fp8_choice = getenv("LAYOVER_PREFILL_FP8");
-    p.stage_fp8 = s.kv_format == LK_FP8_RECORD && !(fp8_choice && strcmp(fp8_choice, "direct") == 0);
+    p.stage_fp8 = unaligned_records || (s.kv_format == LK_FP8_RECORD && !(fp8_choice && strcmp(fp8_choice, "direct") == 0));
     uint32_t wanted = 0;
     if (const char* forced = getenv("LAYOVER_PREFILL_SPLITS")) {
         wanted = uint32_t(strtoul(forced, nullptr, 10));
@@ -787,13 +791,17 @@ void run_prefill(const lk_prefill_shape& s, const void* q, const void* pool, con
     d.head_dim = s.head_dim;
     d.kv_format = s.kv_format;
     const uint64_t block_bytes = pool_block_bytes(d);
-    require(aligned(q, 16) && aligned(out, 16) && aligned(pool, 16) && block_bytes % 16 == 0, "q, out and pool blocks must be 16-byte aligned");
     PrefillPlan p = prefill_plan(s);
     if (!may_split) {
         p.key_splits = 1;
         p.split_steps = uint32_t((((end + kSlots - 1) / kSlots) + 1) / 2);
         p.stage_fp8 = false;
     }
+    // Staged records are read 2 bytes at a time and need only be even; everything read in
+    // place, and q and out, must be 16-byte aligned.
+    require(aligned(q, 16) && aligned(out, 16), "q and out must be 16-byte aligned");
+    require(p.stage_fp8 ? aligned(pool, 2) : aligned(pool, 16) && block_bytes % 16 == 0,
+            p.stage_fp8 ? "FP8 records must be 2-byte aligned" : "pool blocks must be 16-byte aligned");
     const PrefillWorkspace parts = prefill_workspace_parts(s, p);
     const uint64_t need = parts.total();
     require(need == 0 || (workspace != nullptr && workspace_bytes >= need && aligned(workspace, 16)),

@@ -220,8 +220,8 @@ def test_split_keys_match_the_oracle(start, tokens, fp8, splits, monkeypatch):
 )
 def test_prefill_over_drawn_chunks_matches_the_oracle(seed, start, tokens, kv_heads, gqa, layers, fp8, splits):
     """Drawn chunks (start 0-1,500, 1-96 tokens, so chunks begin and end anywhere in a block),
-    1-4 KV heads at GQA 1-5, BF16 pools and FP8 records (refused, unaligned, unless layers x
-    KV heads is a multiple of 4), the split count chosen by the
+    1-4 KV heads at GQA 1-5, BF16 pools and FP8 records (not 16-byte aligned unless layers x
+    KV heads is a multiple of 4: then always staged), the split count chosen by the
     library or forced to 2 or 5; shuffled block ids with spare blocks in the pool. The split
     count is set in the environment around each draw (hypothesis runs every draw inside one
     call of the test, so a fixture could not)."""
@@ -237,7 +237,6 @@ def test_prefill_over_drawn_chunks_matches_the_oracle(seed, start, tokens, kv_he
 
 
 def drawn_prefill_case(seed, start, tokens, kv_heads, gqa, layers, fp8, splits):
-    from layover_amd.kernels._lib import KernelError
     from layover_amd.kernels.hip_prefill import paged_prefill_attention_hip
 
     end = start + tokens
@@ -249,11 +248,33 @@ def drawn_prefill_case(seed, start, tokens, kv_heads, gqa, layers, fp8, splits):
     block_ids = rng.permutation(blocks)[:used].astype(np.int32)
     q = (torch.randn(kv_heads * gqa, tokens, 128, generator=torch.Generator().manual_seed(seed)) * 2).to(torch.bfloat16).cuda()
     print(f"prefill case start={start} tokens={tokens} kv={kv_heads} gqa={gqa} layers={layers} fp8={fp8} splits={splits}", flush=True)
-    if fp8 and (layers * kv_heads) % 4:
-        # Records of 2 x layers x kv_heads groups of 2,050 bytes are not 16-byte aligned.
-        with pytest.raises(KernelError, match="16-byte aligned"):
-            paged_prefill_attention_hip(q, pool, layer, torch.from_numpy(block_ids).cuda(), start, gqa)
-        return
     out = paged_prefill_attention_hip(q, pool, layer, torch.from_numpy(block_ids).cuda(), start, gqa)
     torch.cuda.synchronize()
     assert_close(out, oracle.prefill_attention(q.float().cpu().numpy(), bits, layer, block_ids, start, gqa))
+
+
+@pytest.mark.parametrize("layers,kv_heads", [(1, 1), (3, 2), (5, 1)])
+def test_unaligned_fp8_records_are_staged_and_match_the_oracle(layers, kv_heads):
+    """Records of 2 x layers x kv_heads groups of 2,050 bytes that are not 16-byte aligned are
+    read 2 bytes at a time into the BF16 stage, whatever LAYOVER_PREFILL_FP8 asks; the form
+    without a workspace, which reads records in place, refuses them."""
+    from layover_amd.kernels import _lib
+    from layover_amd.kernels.hip_prefill import paged_prefill_attention_hip
+
+    assert (2 * layers * kv_heads * 2050) % 16
+    start, tokens, gqa = 250, 40, 2
+    used = -(-(start + tokens) // 16)
+    pool, bits = make_pool(used + 1, layers, kv_heads, seed=layers * 10 + kv_heads, fp8=True)
+    block_ids = np.random.default_rng(layers).permutation(used + 1)[:used].astype(np.int32)
+    q = torch.randn(kv_heads * gqa, tokens, 128, device="cuda").to(torch.bfloat16)
+    print(f"unaligned fp8 records layers={layers} kv={kv_heads}", flush=True)
+    out = paged_prefill_attention_hip(q, pool, layers - 1, torch.from_numpy(block_ids).cuda(), start, gqa)
+    torch.cuda.synchronize()
+    assert_close(out, oracle.prefill_attention(q.float().cpu().numpy(), bits, layers - 1, block_ids, start, gqa))
+
+    shape = _lib.PrefillShape(tokens, start, kv_heads * gqa, kv_heads, 128, layers, 16, layers - 1, _lib.LK_BF16, _lib.LK_FP8_RECORD,
+                              1.0 / 128**0.5)
+    lib = _lib.load()
+    ids = torch.from_numpy(block_ids).cuda()
+    status = lib.lk_paged_prefill(shape, q.data_ptr(), pool.records.data_ptr(), ids.data_ptr(), used, out.data_ptr(), None)
+    assert status == _lib.LK_ERR_INVALID and b"16-byte aligned" in lib.lk_last_error()
