@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define LK_ABI_VERSION 2
+#define LK_ABI_VERSION 3
 
 enum { LK_OK = 0, LK_ERR_INVALID = 1, LK_ERR_DEVICE = 2 };
 
@@ -84,7 +84,15 @@ typedef struct {
     float scale;          /* softmax scale, 1/sqrt(head_dim) in the reference */
     uint32_t table_stride;   /* int32 elements between table rows; 0 means table_width */
     uint32_t lengths_stride; /* int32 elements between lengths; 0 means 1 */
+    uint32_t flags;          /* 0, or LK_DECODE_SHARED_BLOCKS */
 } lk_decode_shape;
+
+/* Decode flag: rows of the table share pool blocks (forked prefixes, or tables drawn from a
+ * pool with fewer blocks than they list), so a block read by one row is likely read again by
+ * another soon after. K/V tiles are then loaded so that they stay in the caches (the Infinity
+ * Cache serves the repeats). Without it the tiles are streamed with the non-temporal hint,
+ * the faster form when every block is read once per layer. Results are the same either way. */
+#define LK_DECODE_SHARED_BLOCKS 1u
 
 /* Bytes of device workspace lk_paged_decode needs for this shape (split-K partial results).
  * Depends only on the shape and on the current device's compute-unit count (a grid too small

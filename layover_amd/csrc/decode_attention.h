@@ -108,6 +108,7 @@ struct DecodeArgs {
     uint32_t bps;          // blocks per split
     uint32_t order;        // workgroup order, see decode_unit_of
     uint32_t vector_combine;  // workspace and out aligned for combine_dim128's vector accesses
+    uint32_t shared_blocks;   // LK_DECODE_SHARED_BLOCKS: the cached form of the tile loads
     uint64_t block_bytes;  // bytes from one pool block to the next
     float scale_log2;      // softmax scale * log2(e)
     // Fused decode-time write (lk_paged_decode_append; null write_block: none): row b's new
@@ -217,6 +218,12 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 #ifndef LK_DECODE_RING_FP8
 #define LK_DECODE_RING_FP8 2
 #endif
+// Tile loads of the streaming form (see decode_split_mfma) carry the non-temporal hint.
+template <bool kNT, typename T>
+__device__ __forceinline__ T tile_load(const T* p) {
+    if constexpr (kNT) return __builtin_nontemporal_load(p);
+    else return *p;
+}
 
 // Workgroup -> (sequence, split, KV head). Order 1 (the default): KV head fastest, so the
 // eight heads' tiles of a block (adjacent 4 KiB pieces) are read close together in time, by
@@ -246,7 +253,7 @@ __device__ __forceinline__ bool decode_unit_of(const DecodeArgs& a, uint32_t w, 
 // the FP8 kernel went from 170 to 152 us per layer at batch 32 (0.79 -> 0.89 of 8 TB/s) and
 // from 84.5 to 76 us at batch 64 @ 4,096 (measured on MI355X, A/B in one process). For BF16
 // pools the same request, or three or four waves with a one-tile ring, measured no faster.
-template <int KV, int QF, int kWaves = kDecodeWaves>
+template <int KV, int QF, int kWaves, bool kStream>
 __global__ __launch_bounds__(kWave* kWaves) __attribute__((amdgpu_waves_per_eu(KV == LK_FP8_RECORD ? 2 : 1))) void decode_split_mfma(
     DecodeArgs a) {
     constexpr uint32_t kDecodeWaves = kWaves;
@@ -441,20 +448,66 @@ __global__ __launch_bounds__(kWave* kWaves) __attribute__((amdgpu_waves_per_eu(K
         my_v_shift = shifts[uint64_t(a.layers) * a.kv_heads + head_tile];
     }
 
+    // Two forms of the tile loads (kStream, chosen by the caller's LK_DECODE_SHARED_BLOCKS):
+    // - Streaming (rows read distinct blocks, the usual case): K comes in whole lines -- load
+    //   i, lane l reads bytes 1024 i + 16 l of the K tile -- and relayout() moves the pieces
+    //   through this wave's LDS buffer into the matrix-core layout; V loads already cover
+    //   whole lines (four slot rows each). V, and for FP8 K too, carry the non-temporal hint,
+    //   which keeps the tiles, read once, from allocating in the caches on their way in.
+    //   The hint needs whole lines per load: on the direct K layout (every load instruction
+    //   touching half of each of 16 lines) it made the kernel slower, lines evicted between
+    //   the two halves. Measured per layer on MI355X, Qwen3-4B batch 32 mixed contexts on
+    //   distinct blocks, against the cached form: FP8 207.7 -> 190.1 us (tile probe 180),
+    //   BF16 376.5 -> 357.1 us; FP8 batch 1 @ 32,768 20.4 -> 19.2 us; FP8 batch 64 @ 4,096
+    //   105.3 -> 98.7 us. BF16 K keeps plain loads (non-temporal K measured no faster there).
+    // - Cached (rows share blocks, e.g. forked prefixes or tables drawn from a pool smaller
+    //   than the blocks they list): direct loads in the matrix-core layout, no hint, so a
+    //   block that another row read lately is found in the Infinity Cache. On the 12 GiB pool
+    //   at batch 32: FP8 153.1 against 181.0 us streaming, BF16 290.3 against 294.6 us.
+    // In LDS each slot row's 16-byte pieces are stored at piece ^ (row % pieces per row), so
+    // the reads of 16 lanes, one row each, spread over the banks.
+    constexpr bool kNTK = kStream && KV == LK_FP8_RECORD, kNTV = kStream;
+    constexpr uint32_t kKTile = kSlots * kDim * kElem;
+    constexpr uint32_t kKLoads = kKTile / 1024;               // whole-line K loads per tile
+    constexpr uint32_t kRowPieces = kDim * kElem / 16;        // 16-byte pieces per slot row
+    __shared__ __align__(16) uint8_t s_ktile[kStream ? kDecodeWaves : 1][kStream ? kKTile : 16];
+    const uint64_t k_line_offset = head_tile * tile_bytes + 16 * lane;
+    auto relayout = [&](MfmaTile<KV>& tile) __attribute__((always_inline)) {
+        if constexpr (kStream) {
+            uint8_t* buffer = s_ktile[wave];
+#pragma unroll
+            for (uint32_t i = 0; i < kKLoads; ++i) {
+                const uint32_t row = (1024 * i + 16 * lane) / (kRowPieces * 16), piece = lane % kRowPieces;
+                *reinterpret_cast<u32x4*>(buffer + (row * kRowPieces + (piece ^ (row % kRowPieces))) * 16) =
+                    u32x4{tile.k[4 * i], tile.k[4 * i + 1], tile.k[4 * i + 2], tile.k[4 * i + 3]};
+            }
+            // Lane (g, n) takes the pieces of slot n that the direct loads give it: dims
+            // kGroupDims * g + kStepDims * j for BF16 (piece g + 4j), 32g .. 32g + 31 for FP8
+            // (pieces 2g, 2g + 1).
+#pragma unroll
+            for (uint32_t j = 0; j < kKLoads; ++j) {
+                const uint32_t piece = KV == LK_BF16 ? g + 4 * j : 2 * g + j;
+                const u32x4 w = *reinterpret_cast<const u32x4*>(buffer + (n * kRowPieces + (piece ^ (n % kRowPieces))) * 16);
+#pragma unroll
+                for (int x = 0; x < 4; ++x) tile.k[4 * j + x] = w[x];
+            }
+        }
+    };
     auto fetch_block = [&](MfmaTile<KV>& tile, int32_t block) __attribute__((always_inline)) {
         const uint8_t* base = a.pool + uint64_t(uint32_t(block)) * a.block_bytes;
-        if constexpr (KV == LK_BF16) {
+        if constexpr (kStream) {
+#pragma unroll
+            for (uint32_t i = 0; i < kKLoads; ++i) {
+                const u32x4 w = tile_load<kNTK>(reinterpret_cast<const u32x4*>(base + k_line_offset + 1024 * i));
+#pragma unroll
+                for (int x = 0; x < 4; ++x) tile.k[4 * i + x] = w[x];
+            }
+        } else if constexpr (KV == LK_BF16) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const u32x4 w = *reinterpret_cast<const u32x4*>(base + k_offset + j * MfmaTile<KV>::kStepDims * kElem);
 #pragma unroll
                 for (int x = 0; x < 4; ++x) tile.k[4 * j + x] = w[x];
-            }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const u32x4 w = *reinterpret_cast<const u32x4*>(base + v_offset + uint64_t(r) * kDim * kElem);
-#pragma unroll
-                for (int x = 0; x < 4; ++x) tile.v[r][x] = w[x];
             }
         } else {
 #pragma unroll
@@ -463,9 +516,18 @@ __global__ __launch_bounds__(kWave* kWaves) __attribute__((amdgpu_waves_per_eu(K
 #pragma unroll
                 for (int x = 0; x < 4; ++x) tile.k[4 * j + x] = w[x];
             }
+        }
+        if constexpr (KV == LK_BF16) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const u32x2 w = *reinterpret_cast<const u32x2*>(base + v_offset + uint64_t(r) * kDim * kElem);
+                const u32x4 w = tile_load<kNTV>(reinterpret_cast<const u32x4*>(base + v_offset + uint64_t(r) * kDim * kElem));
+#pragma unroll
+                for (int x = 0; x < 4; ++x) tile.v[r][x] = w[x];
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const u32x2 w = tile_load<kNTV>(reinterpret_cast<const u32x2*>(base + v_offset + uint64_t(r) * kDim * kElem));
                 tile.v[r][0] = w[0];
                 tile.v[r][1] = w[1];
             }
@@ -624,6 +686,7 @@ __global__ __launch_bounds__(kWave* kWaves) __attribute__((amdgpu_waves_per_eu(K
                 if (i + d < mine) {
                     const uint32_t t = wave + (i + d) * kDecodeWaves;
                     shifts_of(ring[d], i + d);
+                    relayout(ring[d]);
                     if (t == count - 1 && wave == writer) written(ring[d]);
                     consume(ring[d], t);
                 }

@@ -188,6 +188,7 @@ void check_shape(const lk_decode_shape& s) {
     require(s.kv_format == LK_BF16 || s.kv_format == LK_F32 || s.kv_format == LK_FP8_RECORD, "unknown KV format");
     require(s.head_dim <= kMaxGenericDim || (s.slots == kSlots && s.head_dim == kDim), "head_dim above 256 is not supported");
     require(s.slots <= 1024, "more than 1024 slots per block is not supported");
+    require((s.flags & ~uint32_t(LK_DECODE_SHARED_BLOCKS)) == 0, "unknown decode flags");
 }
 
 // Workspace: split partials, acc [batch, query_heads, splits, head_dim] then (m, l) pairs.
@@ -210,8 +211,14 @@ uint32_t decode_waves(const DecodeArgs& a, uint64_t grid) {
 template <int KV, int QF>
 void launch_split_mfma(const DecodeArgs& a, uint32_t grid, hipStream_t stream) {
     const uint32_t waves = decode_waves(a, grid);
-    if (waves == 8) hipLaunchKernelGGL((decode_split_mfma<KV, QF, 8>), dim3(grid), dim3(kWave * 8), 0, stream, a);
-    else hipLaunchKernelGGL((decode_split_mfma<KV, QF, 4>), dim3(grid), dim3(kWave * 4), 0, stream, a);
+    const dim3 block(kWave * waves);
+    if (a.shared_blocks) {
+        if (waves == 8) hipLaunchKernelGGL((decode_split_mfma<KV, QF, 8, false>), dim3(grid), block, 0, stream, a);
+        else hipLaunchKernelGGL((decode_split_mfma<KV, QF, 4, false>), dim3(grid), block, 0, stream, a);
+    } else {
+        if (waves == 8) hipLaunchKernelGGL((decode_split_mfma<KV, QF, 8, true>), dim3(grid), block, 0, stream, a);
+        else hipLaunchKernelGGL((decode_split_mfma<KV, QF, 4, true>), dim3(grid), block, 0, stream, a);
+    }
 }
 
 template <int QF>
@@ -320,7 +327,11 @@ __global__ __launch_bounds__(256) void tile_probe(const uint8_t* __restrict__ po
     const u32x4* v = reinterpret_cast<const u32x4*>(base + v_group * kTile);
     u32x4 w = {0, 0, 0, 0};
 #pragma unroll
+#ifdef LK_PROBE_PLAIN
+    for (int i = 0; i < kWords; ++i) w ^= k[i * kWave + lane] ^ v[i * kWave + lane];
+#else
     for (int i = 0; i < kWords; ++i) w ^= __builtin_nontemporal_load(k + i * kWave + lane) ^ __builtin_nontemporal_load(v + i * kWave + lane);
+#endif
     if constexpr (KV == LK_FP8_RECORD) {
         // The two groups' shifts, as the decode loads them (after the record's codes).
         const int16_t* shifts = reinterpret_cast<const int16_t*>(base + 2 * layers * kv_heads * kTile);
@@ -559,6 +570,7 @@ void run_decode(const lk_decode_shape& s, const void* q, const void* pool, const
     a.splits = g.splits;
     a.bps = g.bps;
     a.order = env_order();
+    a.shared_blocks = (s.flags & LK_DECODE_SHARED_BLOCKS) != 0;
     a.vector_combine = aligned(workspace, 16) && aligned(out, s.q_format == LK_BF16 ? 8 : 16);
     a.block_bytes = pool_block_bytes(s);
     a.scale_log2 = s.scale * kLog2e;

@@ -12,9 +12,10 @@ from ctypes import POINTER, c_char_p, c_float, c_int, c_int32, c_uint32, c_uint6
 
 from layover_amd.kv.native import NativeUnavailable, build_dir, hip_runtimes_loaded
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 LK_BF16, LK_F32, LK_FP8_RECORD = 0, 1, 2
 LK_OK, LK_ERR_INVALID, LK_ERR_DEVICE = 0, 1, 2
+LK_DECODE_SHARED_BLOCKS = 1
 LIBRARY_NAME = "liblayover_kernels.so"
 
 
@@ -41,6 +42,7 @@ class DecodeShape(ctypes.Structure):
         ("scale", c_float),
         ("table_stride", c_uint32),
         ("lengths_stride", c_uint32),
+        ("flags", c_uint32),
     ]
 
 

@@ -168,30 +168,37 @@ def validate_shapes(q, pool, layer, block_table, lengths, kv_groups) -> None:
         raise ValueError(f"head_dim {head_dim} is not supported (at most 256)")
 
 
-def validate(q, pool, layer, block_table, lengths, kv_groups) -> None:
+def validate(q, pool, layer, block_table, lengths, kv_groups) -> int:
     """validate_shapes plus the bounds a kernel cannot check for itself, at the cost of one
-    device read (triton_decode.py:218-232)."""
+    device read (triton_decode.py:218-232). Returns the number of table entries the lengths
+    cover (blocks the launch reads, counted once per row), taken in the same read."""
     validate_shapes(q, pool, layer, block_table, lengths, kv_groups)
     slots, blocks = pool.shape[4], pool.shape[0]
-    bounds = torch.stack([*torch.aminmax(lengths.long()), *torch.aminmax(block_table.long())])
-    shortest, longest, lowest, highest = bounds.tolist()
+    wide = lengths.long()
+    listed = torch.div(wide + slots - 1, slots, rounding_mode="floor").sum()
+    bounds = torch.stack([*torch.aminmax(wide), *torch.aminmax(block_table.long()), listed])
+    shortest, longest, lowest, highest, listed = bounds.tolist()
     if shortest < 1 or longest > block_table.shape[1] * slots:
         raise ValueError(f"lengths in [{shortest}, {longest}] do not fit a table of {block_table.shape[1]} blocks")
     if lowest < 0 or highest >= blocks:
         raise ValueError(f"block ids in [{lowest}, {highest}] are outside a pool of {blocks} blocks")
+    return listed
 
 
-def decode_shape(q, pool, layer, block_table, kv_groups, lengths=None) -> _lib.DecodeShape:
+def decode_shape(q, pool, layer, block_table, kv_groups, lengths=None, shared_blocks: bool = False) -> _lib.DecodeShape:
     """The launch's shape; the table's row stride and the lengths' stride are taken from the
     tensors, so columns of a packed row block (PagedKVCache.decode_rows) pass without a copy,
-    as the reference's launcher passes strides (triton_decode.py:131-179)."""
+    as the reference's launcher passes strides (triton_decode.py:131-179). shared_blocks sets
+    LK_DECODE_SHARED_BLOCKS: rows read some of the same blocks, so the kernel keeps tiles in
+    the caches instead of streaming them (the same results, a different speed)."""
     batch, query_heads, head_dim = q.shape
     _, _, layers, kv_heads, slots, _ = pool.shape
     kv_format = _lib.LK_FP8_RECORD if _is_fp8(pool) else _FORMATS[pool.dtype]
     table_stride = block_table.stride(0) if block_table.dim() == 2 else block_table.shape[-1]
     lengths_stride = lengths.stride(0) if lengths is not None and lengths.dim() == 1 else 1
     return _lib.DecodeShape(batch, query_heads, kv_heads, head_dim, layers, slots, layer, block_table.shape[1],
-                            _FORMATS[q.dtype], kv_format, 1.0 / math.sqrt(head_dim), table_stride, lengths_stride)
+                            _FORMATS[q.dtype], kv_format, 1.0 / math.sqrt(head_dim), table_stride, lengths_stride,
+                            _lib.LK_DECODE_SHARED_BLOCKS if shared_blocks else 0)
 
 
 def _check_layout(q, block_table, lengths, out) -> None:
@@ -213,13 +220,14 @@ def workspace_bytes(shape: _lib.DecodeShape) -> int:
     return int(_lib.load().lk_paged_decode_workspace(shape))
 
 
-def run_kernel(q, pool, layer, block_table, lengths, kv_groups, out, workspace=None) -> None:
+def run_kernel(q, pool, layer, block_table, lengths, kv_groups, out, workspace=None, shared_blocks: bool = False) -> None:
     """Launch without validating values, on the current stream. q and out contiguous; table
     int32 [batch, width] with contiguous rows at any row stride; lengths int32 [batch] at any
-    stride. A workspace passed in must not be in use by another launch at the same time."""
+    stride. A workspace passed in must not be in use by another launch at the same time.
+    shared_blocks as for decode_shape."""
     _check_layout(q, block_table, lengths, out)
     lib = _lib.load()
-    shape = decode_shape(q, pool, layer, block_table, kv_groups, lengths)
+    shape = decode_shape(q, pool, layer, block_table, kv_groups, lengths, shared_blocks)
     need = int(lib.lk_paged_decode_workspace(shape))
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=q.device)
@@ -230,13 +238,15 @@ def run_kernel(q, pool, layer, block_table, lengths, kv_groups, out, workspace=N
     )
 
 
-def run_kernel_append(q, pool, layer, block_table, lengths, kv_groups, write_blocks, write_slots, k, v, out, workspace=None) -> None:
+def run_kernel_append(q, pool, layer, block_table, lengths, kv_groups, write_blocks, write_slots, k, v, out, workspace=None,
+                      shared_blocks: bool = False) -> None:
     """write_tokens (BF16 pool) or Fp8KVPool.write (FP8 records) of each row's new token into
     `layer`, then run_kernel of that layer, as one decode launch where the shape allows
     (lk_paged_decode_append). The write position must be the row's last token, as the first
     two columns of PagedKVCache.decode_rows give it; that is not checked. Rows must name
     distinct blocks, and a row's token is written only if 1 <= its length <= the table's
-    width x slots (decode_rows guarantees both). Enqueued on the current stream."""
+    width x slots (decode_rows guarantees both). Enqueued on the current stream. shared_blocks
+    as for decode_shape."""
     _check_layout(q, block_table, lengths, out)
     if _is_fp8(pool):
         storage, layers, kv_heads, head_dim = pool.records, pool.layers, pool.kv_heads, pool.head_dim
@@ -248,7 +258,7 @@ def run_kernel_append(q, pool, layer, block_table, lengths, kv_groups, write_blo
     if batch != q.shape[0]:
         raise ValueError("one written token per decode row")
     lib = _lib.load()
-    shape = decode_shape(q, pool, layer, block_table, kv_groups, lengths)
+    shape = decode_shape(q, pool, layer, block_table, kv_groups, lengths, shared_blocks)
     need = int(lib.lk_paged_decode_workspace(shape))
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(max(need, 4), dtype=torch.uint8, device=q.device)
@@ -259,23 +269,28 @@ def run_kernel_append(q, pool, layer, block_table, lengths, kv_groups, write_blo
     )
 
 
-def _launch(q, pool, layer, block_table, lengths, kv_groups) -> torch.Tensor:
+def _launch(q, pool, layer, block_table, lengths, kv_groups, shared_blocks: bool) -> torch.Tensor:
     q = q.contiguous()
     block_table = block_table.to(torch.int32).contiguous()
     lengths = lengths.to(torch.int32).contiguous()
     out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-    run_kernel(q, pool, layer, block_table, lengths, kv_groups, out)
+    run_kernel(q, pool, layer, block_table, lengths, kv_groups, out, shared_blocks=shared_blocks)
     return out
 
 
-def paged_decode_attention_hip(q, pool, layer, block_table, lengths, kv_groups) -> torch.Tensor:
-    """Drop-in for paged_decode_attention_triton: validated, result in q's dtype and device."""
-    validate(q, pool, layer, block_table, lengths, kv_groups)
-    return _launch(q, pool, layer, block_table, lengths, kv_groups)
+def paged_decode_attention_hip(q, pool, layer, block_table, lengths, kv_groups, shared_blocks: bool | None = None) -> torch.Tensor:
+    """Drop-in for paged_decode_attention_triton: validated, result in q's dtype and device.
+    shared_blocks (see decode_shape) left as None is decided from the validation's read-back:
+    rows listing more blocks than the pool holds must share some of them."""
+    listed = validate(q, pool, layer, block_table, lengths, kv_groups)
+    if shared_blocks is None:
+        shared_blocks = listed > pool.shape[0]
+    return _launch(q, pool, layer, block_table, lengths, kv_groups, shared_blocks)
 
 
-def paged_decode_attention_hip_trusted(q, pool, layer, block_table, lengths, kv_groups) -> torch.Tensor:
+def paged_decode_attention_hip_trusted(q, pool, layer, block_table, lengths, kv_groups, shared_blocks: bool = False) -> torch.Tensor:
     """For tables whose lengths and ids the caller checked on the host (as
-    PagedKVCache.decode_batch does): reads nothing back from the GPU."""
+    PagedKVCache.decode_batch does): reads nothing back from the GPU. shared_blocks as for
+    decode_shape; the caller knows whether its rows share blocks (forked prefixes)."""
     validate_shapes(q, pool, layer, block_table, lengths, kv_groups)
-    return _launch(q, pool, layer, block_table, lengths, kv_groups)
+    return _launch(q, pool, layer, block_table, lengths, kv_groups, shared_blocks)

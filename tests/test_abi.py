@@ -56,7 +56,7 @@ def test_hip_libraries_load_into_one_hip_runtime_without_a_gpu():
     lib = native.load_library("hip")
     assert lib.lt_abi_version() == 2 and lib.lt_flavor() == b"hip"
     kernels = _lib.load()
-    assert kernels.lk_abi_version() == 2
+    assert kernels.lk_abi_version() == 3
     assert len(native.hip_runtimes_loaded()) == 1
 
 

@@ -39,7 +39,7 @@ def test_kernel_library_loads_into_torchs_hip_runtime():
 
     torch.zeros(1, device="cuda")
     lib = _lib.load()
-    assert lib.lk_abi_version() == 2
+    assert lib.lk_abi_version() == 3
     assert load_library("hip").lt_flavor() == b"hip"
     assert len(hip_runtimes_loaded()) == 1, hip_runtimes_loaded()
 
@@ -547,3 +547,82 @@ def test_decode_with_one_split_writes_the_output_itself_bit_for_bit(fp8, hip_dec
         expected = oracle.decode_attention(q, reference_pool, layer, table, lens, 4)
         weighted = weighted_mean_abs_v(q, reference_pool, layer, table, lens, 4) if kv == "fp8" else None
         assert_close_to_oracle(direct.float(), expected, f"{kv} layer {layer}", weight_rounding=weighted)
+
+
+@pytest.mark.parametrize("kv", ["bf16", "fp8"])
+@pytest.mark.parametrize("q_format", ["bf16", "f32"])
+@pytest.mark.parametrize("grid", ["small", "large"])
+def test_streaming_and_cached_tile_loads_agree_bit_for_bit(fp8, hip_decode, kv, q_format, grid):
+    """LK_DECODE_SHARED_BLOCKS switches the matrix-core kernel between two forms of its tile
+    loads: streaming (K loaded in whole lines and laid out through LDS, non-temporal hints)
+    and cached (K loaded in the matrix-core layout directly). The values reaching the matrix
+    cores are the same, so outputs are identical, on the 8-wave kernel of small grids and the
+    4-wave kernel of large ones (64 rows x 8 KV heads x 2 splits = 1,024 workgroups), with
+    ragged lengths and with the fused token write. The small case is also checked against the
+    oracle (the streaming form is the default every other decode test runs)."""
+    from layover_amd.kernels import _lib
+
+    layers, kv_heads, groups = 2, 8, 4
+    if grid == "small":
+        lengths = [1, 17, 300, 2049, 777]
+        blocks = 5 * 129 + 5
+    else:
+        rng = np.random.default_rng(5)
+        lengths = [int(n) for n in rng.integers(1, 2049, size=64)]
+        lengths[0] = 2048
+        blocks = 64 * 128 + 8
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    pool = torch.randn(blocks, 2, layers, kv_heads, 16, 128, generator=gen, device="cuda").to(torch.bfloat16)
+    width = max(-(-n // 16) for n in lengths)
+    table = torch.randperm(blocks, generator=gen, device="cuda")[: len(lengths) * width].view(len(lengths), width).to(torch.int32)
+    lens = torch.tensor(lengths, dtype=torch.int32, device="cuda")
+    q = torch.randn(len(lengths), kv_heads * groups, 128, generator=gen, device="cuda")
+    q = q.to(torch.bfloat16) if q_format == "bf16" else q
+    if kv == "bf16":
+        target = pool
+    else:
+        layout = fp8.Fp8Layout(16 * 128, 2 * layers * kv_heads)
+        records = torch.empty(blocks, layout.record_bytes, dtype=torch.uint8, device="cuda")
+        fp8.quantize_blocks(pool, torch.arange(blocks, dtype=torch.int32, device="cuda"), records.view(-1), layout)
+        target = hip_decode.Fp8KVPool(records, layers, kv_heads, 16, 128)
+    shape = hip_decode.decode_shape(q, target, 1, table, groups, lens)
+    splits = int(_lib.load().lk_paged_decode_workspace(shape)) // (len(lengths) * kv_heads * groups * 130 * 4)
+    if grid == "large":
+        assert len(lengths) * splits * kv_heads >= 1024, splits
+    print(f"streaming vs cached: {kv} q {q_format} {grid} grid, {splits} splits", flush=True)
+    bits = lambda t: t.view(torch.int16) if q_format == "bf16" else t.view(torch.int32)
+    outs = {}
+    for shared in (False, True):
+        out = torch.empty_like(q)
+        hip_decode.run_kernel(q, target, 1, table, lens, groups, out, shared_blocks=shared)
+        outs[shared] = out
+    torch.cuda.synchronize()
+    assert torch.equal(bits(outs[False]), bits(outs[True]))
+    # The fused write of each row's last token (write position = the last token), both forms,
+    # each on its own copy of the pool: pools and outputs equal.
+    last = (lens - 1).long()
+    write_blocks = table.gather(1, (last // 16).view(-1, 1)).view(-1).contiguous()
+    write_slots = (last % 16).to(torch.int32).contiguous()
+    k_new = torch.randn(len(lengths), kv_heads, 128, generator=gen, device="cuda").to(torch.bfloat16)
+    v_new = torch.randn(len(lengths), kv_heads, 128, generator=gen, device="cuda").to(torch.bfloat16)
+    results = {}
+    for shared in (False, True):
+        copy = target.clone() if kv == "bf16" else hip_decode.Fp8KVPool(target.records.clone(), layers, kv_heads, 16, 128)
+        out = torch.empty_like(q)
+        hip_decode.run_kernel_append(q, copy, 1, table, lens, groups, write_blocks, write_slots, k_new, v_new, out, shared_blocks=shared)
+        results[shared] = (out, copy if kv == "bf16" else copy.records)
+    torch.cuda.synchronize()
+    assert torch.equal(bits(results[False][0]), bits(results[True][0]))
+    assert torch.equal(results[False][1].view(torch.uint8), results[True][1].view(torch.uint8))
+    if grid == "small" and q_format == "bf16":
+        q_bits = q.cpu().view(torch.int16).numpy().view(np.uint16)
+        if kv == "bf16":
+            pool_bits = pool.cpu().view(torch.int16).numpy().view(np.uint16)
+        else:
+            pool_bits = np.zeros((blocks, 2, layers, kv_heads, 16, 128), dtype=np.uint16)
+            oracle.dequantize_records(target.records.cpu().numpy().reshape(-1), np.arange(blocks, dtype=np.int32), pool_bits,
+                                      16 * 128, 2 * layers * kv_heads)
+        table_np, lens_np = table.cpu().numpy(), lens.cpu().numpy()
+        expected = oracle.decode_attention(q_bits, pool_bits, 1, table_np, lens_np, groups)
+        weighted = weighted_mean_abs_v(q_bits, pool_bits, 1, table_np, lens_np, groups) if kv == "fp8" else None
+        assert_close_to_oracle(outs[False].float(), expected, f"streaming {kv}", weight_rounding=weighted)
