@@ -393,12 +393,15 @@ def decode_tables(rng, batch: int, lengths, pool_blocks: int, distinct: bool):
 
 def decode_bench(device, pool, lengths, steps: int, warmup: int, seed: int, distinct: bool = False, kv_pool=None, probe: bool = True,
                  pool_blocks: int | None = None):
-    """Time 36 single-layer launches per step; bytes are the reference's unique accounting.
-    `pool` (BF16) may be None when `kv_pool` (FP8 records) and `pool_blocks` are given."""
+    """Time 36 single-layer launches per step; bytes are the reference's unique accounting
+    (layover_amd.kernels.decode_bytes). `pool` (BF16) may be None when `kv_pool` (FP8 records)
+    and `pool_blocks` are given. Rows whose tables list more blocks than the pool holds share
+    blocks, and are launched with LK_DECODE_SHARED_BLOCKS, as paged_decode_attention_hip
+    decides it; otherwise the tiles are streamed."""
     import numpy as np
     import torch
 
-    from layover_amd.kernels import hip_decode
+    from layover_amd.kernels import decode_bytes, hip_decode
 
     rng = np.random.default_rng(seed)
     batch = len(lengths)
@@ -409,35 +412,35 @@ def decode_bench(device, pool, lengths, steps: int, warmup: int, seed: int, dist
     q = torch.randn(batch, QWEN["query_heads"], QWEN["head_dim"], generator=generator, device=device).to(torch.bfloat16)
     target = kv_pool if kv_pool is not None else pool
     out = torch.empty_like(q)
+    shared = decode_bytes.sequence_blocks(lengths, QWEN["slots"]) > pool_blocks
     shape = hip_decode.decode_shape(q, target, 0, table, QWEN["query_heads"] // QWEN["kv_heads"])
     workspace = torch.empty(hip_decode.workspace_bytes(shape), dtype=torch.uint8, device=device)
     groups = QWEN["query_heads"] // QWEN["kv_heads"]
     for _ in range(warmup):
         for layer in range(QWEN["layers"]):
-            hip_decode.run_kernel(q, target, layer, table, lens, groups, out, workspace)
+            hip_decode.run_kernel(q, target, layer, table, lens, groups, out, workspace, shared_blocks=shared)
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(steps):
         for layer in range(QWEN["layers"]):
-            hip_decode.run_kernel(q, target, layer, table, lens, groups, out, workspace)
+            hip_decode.run_kernel(q, target, layer, table, lens, groups, out, workspace, shared_blocks=shared)
     end.record()
     end.synchronize()
     per_layer_ms = start.elapsed_time(end) / (steps * QWEN["layers"])
-    blocks = sum(-(-int(n) // 16) for n in lengths)
-    tile = QWEN["slots"] * QWEN["head_dim"]
-    if kv_pool is not None:
-        kv_bytes = blocks * QWEN["kv_heads"] * 2 * (tile + 2)
-    else:
-        kv_bytes = blocks * QWEN["kv_heads"] * 2 * tile * 2
-    other = q.numel() * 2 * 2 + table.numel() * 4 + batch * 4
+    kv_format = "fp8" if kv_pool is not None else "bf16"
+    kv_bytes = (decode_bytes.fp8_record_bytes_per_layer(lengths, decode_bytes.QWEN3_4B) if kv_pool is not None
+                else decode_bytes.unique_bytes_per_layer(lengths, decode_bytes.QWEN3_4B, 2))
+    launch = decode_bytes.launch_bytes(lengths, decode_bytes.QWEN3_4B, kv_format, 2, table.shape[1])
     result = {
         "batch": batch,
         "per_layer_us": per_layer_ms * 1e3,
         "kv_bytes_per_layer": kv_bytes,
-        "achieved_gbs": (kv_bytes + other) / (per_layer_ms * 1e-3) / 1e9,
-        "frac_of_hbm_peak": (kv_bytes + other) / (per_layer_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "launch_bytes": launch,
+        "achieved_gbs": launch / (per_layer_ms * 1e-3) / 1e9,
+        "frac_of_hbm_peak": launch / (per_layer_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "distinct_blocks": distinct,
+        "shared_blocks": shared,
     }
     if not probe:
         return result
@@ -466,7 +469,7 @@ def decode_bench(device, pool, lengths, steps: int, warmup: int, seed: int, dist
     return result
 
 
-def decode_step_events(device, pool, table, lens, q, out, workspace, groups):
+def decode_step_events(device, pool, table, lens, q, out, workspace, groups, shared_blocks: bool):
     """Launch one decode step (36 single-layer launches) on the current stream, bracketed by
     timing events; returns the events."""
     import torch
@@ -476,7 +479,7 @@ def decode_step_events(device, pool, table, lens, q, out, workspace, groups):
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for layer in range(QWEN["layers"]):
-        hip_decode.run_kernel(q, pool, layer, table, lens, groups, out, workspace)
+        hip_decode.run_kernel(q, pool, layer, table, lens, groups, out, workspace, shared_blocks=shared_blocks)
     end.record()
     return start, end
 
@@ -488,6 +491,7 @@ def graph_decode_bench(device, cache, fp8_pool, steps: int = 20) -> list:
     import numpy as np
     import torch
 
+    from layover_amd.kernels import decode_bytes
     from layover_amd.kv.decode_graphs import DecodeAttentionGraphs
     from layover_amd.kv.paged_cache import BlockTable
 
@@ -515,14 +519,15 @@ def graph_decode_bench(device, cache, fp8_pool, steps: int = 20) -> list:
                 end.record()
                 end.synchronize()
                 timings[mode] = start.elapsed_time(end) / steps
-            tile = QWEN["slots"] * QWEN["head_dim"]
-            per_block = QWEN["kv_heads"] * 2 * ((tile + 2) if kind == "fp8" else tile * 2)
-            kv_bytes = batch * need * per_block
+            lengths = [tokens] * batch
+            kv_bytes = (decode_bytes.fp8_record_bytes_per_layer(lengths, decode_bytes.QWEN3_4B) if kind == "fp8"
+                        else decode_bytes.unique_bytes_per_layer(lengths, decode_bytes.QWEN3_4B, 2))
             runs.append({
                 "case": f"{kind}_batch{batch}_{tokens}",
                 "graph_per_layer_us": round(timings["graph"] * 1e3 / QWEN["layers"], 2),
                 "eager_per_layer_us": round(timings["eager"] * 1e3 / QWEN["layers"], 2),
                 "graph_kv_gbs": round(kv_bytes / (timings["graph"] * 1e-3 / QWEN["layers"]) / 1e9, 1),
+                "graph_frac_of_hbm_peak": round(kv_bytes / (timings["graph"] * 1e-3 / QWEN["layers"]) / 1e9 / HBM_PEAK_GBS, 4),
                 "captured_size": size,
                 "captured_width": width,
             })
@@ -617,7 +622,7 @@ def overlap_bench(device, cache, pool_blocks: int, swap_blocks: int = 2048, stag
     import numpy as np
     import torch
 
-    from layover_amd.kernels import hip_decode
+    from layover_amd.kernels import decode_bytes, hip_decode
     from layover_amd.kv.transfer import NativeBackend
 
     rng = np.random.default_rng(7)
@@ -630,7 +635,8 @@ def overlap_bench(device, cache, pool_blocks: int, swap_blocks: int = 2048, stag
     groups = QWEN["query_heads"] // QWEN["kv_heads"]
     shape = hip_decode.decode_shape(q, cache.pool, 0, table, groups)
     workspace = torch.empty(hip_decode.workspace_bytes(shape), dtype=torch.uint8, device=device)
-    step = lambda: decode_step_events(device, cache.pool, table, lens, q, out, workspace, groups)
+    shared = decode_bytes.sequence_blocks(lengths, QWEN["slots"]) > decode_region  # rows drawn from a smaller region share blocks
+    step = lambda: decode_step_events(device, cache.pool, table, lens, q, out, workspace, groups, shared)
 
     for _ in range(2):
         step()
@@ -671,19 +677,26 @@ def overlap_bench(device, cache, pool_blocks: int, swap_blocks: int = 2048, stag
     payload = out_ticket.payload
     in_ticket, in_ms, in_steps = overlapped(lambda: backend.start_in(cache, dst, payload))
     torch.cuda.synchronize()
-    during = [s.elapsed_time(e) for s, e in out_steps + in_steps]
+    during_out = [s.elapsed_time(e) for s, e in out_steps]
+    during_in = [s.elapsed_time(e) for s, e in in_steps]
+    during = during_out + during_in
     backend.free(payload)
     backend.close()
     record = 1_180_800
-    blocks = sum(-(-n // 16) for n in lengths)
-    kv_bytes = blocks * QWEN["kv_heads"] * 2 * 16 * 128 * 2 * QWEN["layers"]
+    kv_bytes = decode_bytes.unique_bytes_per_layer(lengths, decode_bytes.QWEN3_4B, 2) * QWEN["layers"]
     overlap_ms = out_ms + in_ms
     decode_during_ms = sum(during) / max(1, len(during))
+    mean = lambda xs: sum(xs) / max(1, len(xs))
     return {
         "decode_step_solo_ms": round(solo_ms, 3),
         "decode_step_during_swap_ms": round(decode_during_ms, 3),
         "decode_inflation_pct": round(100 * (decode_during_ms / solo_ms - 1), 1),
+        "decode_inflation_during_swap_out_pct": round(100 * (mean(during_out) / solo_ms - 1), 1),
+        "decode_inflation_during_swap_in_pct": round(100 * (mean(during_in) / solo_ms - 1), 1),
         "decode_steps_during_swap": len(during),
+        "decode_steps_during_swap_out": len(during_out),
+        "decode_steps_during_swap_in": len(during_in),
+        "shared_blocks": shared,
         "swap_out_ms": round(out_ms, 2),
         "swap_in_ms": round(in_ms, 2),
         "swap_blocks": swap_blocks,
@@ -1047,8 +1060,11 @@ def main() -> None:
         mixed = [int(n) for n in rng.integers(1024, 32769, size=32)]
         log("decode bf16 (config 3)")
         decode = decode_bench(device, cache.pool, mixed, args.decode_steps, 1, seed=3)
-        result["decode"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in decode.items()}
-        result["decode"]["lengths"] = "U[1024, 32768], batch 32, seed 2; rows sampled from the 12 GiB pool (blocks alias across rows)"
+        # Config 3 as stated: rows drawn from the 12 GiB pool, so they share blocks and some
+        # reads are served by the Infinity Cache. The headline `decode` is the distinct-block
+        # run below (every byte from DRAM); this one is kept beside it.
+        result["decode_aliased"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in decode.items()}
+        result["decode_aliased"]["lengths"] = "U[1024, 32768], batch 32, seed 2; rows sampled from the 12 GiB pool (blocks alias across rows)"
         log("decode fp8 records (config 4)")
         records = torch.empty(pool_blocks, layout.record_bytes, dtype=torch.uint8, device=device)
         for first in range(0, pool_blocks, 512):
@@ -1056,7 +1072,7 @@ def main() -> None:
             quantize_blocks(cache.pool, ids, records[first:].reshape(-1), layout)
         fp8_pool = Fp8KVPool(records, config.num_hidden_layers, config.num_key_value_heads, 16, config.head_dim)
         fp8_runs = []
-        for name, lengths in (("batch32_mixed", mixed), ("batch1_32768", [32768]), ("batch64_4096", [4096] * 64)):
+        for name, lengths in (("batch32_mixed_aliased", mixed), ("batch1_32768", [32768]), ("batch64_4096", [4096] * 64)):
             run = decode_bench(device, cache.pool, lengths, args.decode_steps, 1, seed=4, kv_pool=fp8_pool)
             fp8_runs.append({"case": name, **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in run.items()}})
         result["decode_fp8"] = fp8_runs
@@ -1080,7 +1096,12 @@ def main() -> None:
         result["overlap"] = overlap_bench(device, cache, pool_blocks)
     if not args.skip_decode and not args.skip_distinct:
         log("decode on distinct blocks (~80 GB pool)")
-        result["decode_distinct"], result["decode_fp8_distinct"] = distinct_decode(device, args.decode_steps)
+        bf16_distinct, fp8_distinct = distinct_decode(device, args.decode_steps)
+        bf16_distinct["lengths"] = "U[1024, 32768], batch 32, seed 2; every table entry a distinct block (no Infinity Cache reuse)"
+        result["decode"] = bf16_distinct
+        result["decode_fp8"].insert(0, {"case": "batch32_mixed", **fp8_distinct})
+    elif "decode_aliased" in result:
+        result["decode"] = result["decode_aliased"]
 
     # Last, so its 12 GiB of buffers come and go after everything timed above.
     log("HBM probe")

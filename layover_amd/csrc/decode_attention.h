@@ -218,11 +218,21 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 #ifndef LK_DECODE_RING_FP8
 #define LK_DECODE_RING_FP8 2
 #endif
-// Tile loads of the streaming form (see decode_split_mfma) carry the non-temporal hint.
-template <bool kNT, typename T>
-__device__ __forceinline__ T tile_load(const T* p) {
-    if constexpr (kNT) return __builtin_nontemporal_load(p);
-    else return *p;
+// Tile loads go through a buffer resource that spans one pool block (base and size in
+// scalar registers, offsets per lane). A resource of size 0 turns every load into zeros that
+// touch no memory: the ring's refills past a wave's last unit cost nothing, yet every load is
+// still issued unconditionally, so the compiler's wait counts stay exact. The streaming form
+// (see decode_split_mfma) sets the non-temporal bit.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t block_resource(const uint8_t* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), short(0), int(bytes), 0x00020000);
+}
+template <bool kNT>
+__device__ __forceinline__ u32x4 tile_load16(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, kNT ? 2 : 0));
+}
+template <bool kNT>
+__device__ __forceinline__ u32x2 tile_load8(__amdgpu_buffer_rsrc_t r, uint32_t offset) {
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, offset, 0, kNT ? 2 : 0));
 }
 
 // Workgroup -> (sequence, split, KV head). Order 1 (the default): KV head fastest, so the
@@ -493,47 +503,41 @@ __global__ __launch_bounds__(kWave* kWaves) __attribute__((amdgpu_waves_per_eu(K
             }
         }
     };
-    auto fetch_block = [&](MfmaTile<KV>& tile, int32_t block) __attribute__((always_inline)) {
-        const uint8_t* base = a.pool + uint64_t(uint32_t(block)) * a.block_bytes;
+    // Unit i of this wave into a ring buffer; i at or past the wave's units (the ring's
+    // refills after its last unit) loads zeros from an empty resource.
+    const uint32_t k_first = uint32_t(kStream ? k_line_offset : k_offset), v_first = uint32_t(v_offset);
+    auto fetch = [&](MfmaTile<KV>& tile, uint32_t i) __attribute__((always_inline)) {
+        const uint32_t block = uint32_t(__builtin_amdgcn_readlane(my_block, min(i, mine - 1)));
+        const __amdgpu_buffer_rsrc_t r = block_resource(a.pool + uint64_t(block) * a.block_bytes, i < mine ? uint32_t(a.block_bytes) : 0u);
         if constexpr (kStream) {
 #pragma unroll
-            for (uint32_t i = 0; i < kKLoads; ++i) {
-                const u32x4 w = tile_load<kNTK>(reinterpret_cast<const u32x4*>(base + k_line_offset + 1024 * i));
+            for (uint32_t x = 0; x < kKLoads; ++x) {
+                const u32x4 w = tile_load16<kNTK>(r, k_first + 1024 * x);
 #pragma unroll
-                for (int x = 0; x < 4; ++x) tile.k[4 * i + x] = w[x];
-            }
-        } else if constexpr (KV == LK_BF16) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const u32x4 w = *reinterpret_cast<const u32x4*>(base + k_offset + j * MfmaTile<KV>::kStepDims * kElem);
-#pragma unroll
-                for (int x = 0; x < 4; ++x) tile.k[4 * j + x] = w[x];
+                for (int y = 0; y < 4; ++y) tile.k[4 * x + y] = w[y];
             }
         } else {
+            constexpr uint32_t kStep = KV == LK_BF16 ? MfmaTile<KV>::kStepDims * kElem : 16;
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const u32x4 w = reinterpret_cast<const u32x4*>(base + k_offset)[j];
+            for (uint32_t x = 0; x < kKLoads; ++x) {
+                const u32x4 w = tile_load16<false>(r, k_first + kStep * x);
 #pragma unroll
-                for (int x = 0; x < 4; ++x) tile.k[4 * j + x] = w[x];
+                for (int y = 0; y < 4; ++y) tile.k[4 * x + y] = w[y];
             }
         }
-        if constexpr (KV == LK_BF16) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const u32x4 w = tile_load<kNTV>(reinterpret_cast<const u32x4*>(base + v_offset + uint64_t(r) * kDim * kElem));
+        for (uint32_t row = 0; row < 4; ++row) {
+            if constexpr (KV == LK_BF16) {
+                const u32x4 w = tile_load16<kNTV>(r, v_first + row * kDim * kElem);
 #pragma unroll
-                for (int x = 0; x < 4; ++x) tile.v[r][x] = w[x];
-            }
-        } else {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const u32x2 w = tile_load<kNTV>(reinterpret_cast<const u32x2*>(base + v_offset + uint64_t(r) * kDim * kElem));
-                tile.v[r][0] = w[0];
-                tile.v[r][1] = w[1];
+                for (int y = 0; y < 4; ++y) tile.v[row][y] = w[y];
+            } else {
+                const u32x2 w = tile_load8<kNTV>(r, v_first + row * kDim * kElem);
+                tile.v[row][0] = w[0];
+                tile.v[row][1] = w[1];
             }
         }
     };
-    auto fetch = [&](MfmaTile<KV>& tile, uint32_t i) __attribute__((always_inline)) { fetch_block(tile, __builtin_amdgcn_readlane(my_block, i)); };
     // The shifts of the wave's unit i, taken when the unit is consumed.
     auto shifts_of = [&](MfmaTile<KV>& tile, uint32_t i) __attribute__((always_inline)) {
         if constexpr (KV == LK_FP8_RECORD) {
@@ -670,15 +674,21 @@ __global__ __launch_bounds__(kWave* kWaves) __attribute__((amdgpu_waves_per_eu(K
     };
 
     // A ring of kRing register buffers, each refilled as soon as it is consumed. Refills are
-    // unconditional: past the wave's last unit they re-read that unit (an L2 hit), because a
-    // conditional load would make every later wait assume it might not have been issued,
-    // i.e. wait for all loads in flight.
-    constexpr int kRing = KV == LK_BF16 ? LK_DECODE_RING_BF16 : LK_DECODE_RING_FP8;
+    // unconditional (past the wave's last unit, from an empty resource: zeros, no memory
+    // access), because a conditional load would make every later wait assume it might not
+    // have been issued, i.e. wait for all loads in flight.
+#ifndef LK_DECODE_RING8_BF16
+#define LK_DECODE_RING8_BF16 LK_DECODE_RING_BF16
+#endif
+#ifndef LK_DECODE_RING8_FP8
+#define LK_DECODE_RING8_FP8 LK_DECODE_RING_FP8
+#endif
+    constexpr int kRing = kWaves == 8 ? (KV == LK_BF16 ? LK_DECODE_RING8_BF16 : LK_DECODE_RING8_FP8)
+                                      : (KV == LK_BF16 ? LK_DECODE_RING_BF16 : LK_DECODE_RING_FP8);
     MfmaTile<KV> ring[kRing];
     if (mine > 0) {
-        const uint32_t last = mine - 1;
 #pragma unroll
-        for (int d = 0; d < kRing; ++d) fetch(ring[d], min(uint32_t(d), last));
+        for (int d = 0; d < kRing; ++d) fetch(ring[d], uint32_t(d));
         if (kLateEncode && wave == writer) reencode();
         for (uint32_t i = 0; i < mine; i += kRing) {
 #pragma unroll
@@ -690,7 +700,7 @@ __global__ __launch_bounds__(kWave* kWaves) __attribute__((amdgpu_waves_per_eu(K
                     if (t == count - 1 && wave == writer) written(ring[d]);
                     consume(ring[d], t);
                 }
-                fetch(ring[d], min(i + d + kRing, last));
+                fetch(ring[d], i + d + kRing);
             }
         }
     }

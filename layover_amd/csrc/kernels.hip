@@ -139,12 +139,13 @@ uint64_t pool_block_bytes(const lk_decode_shape& s) {
 }
 
 // The matrix-core kernel needs the Qwen3 tile shape (16 slots x 128 dims), at most 16 query
-// heads per KV head, a BF16 or FP8-record pool and 16-byte aligned tiles (pool base and block
-// stride); anything else runs the generic kernel.
+// heads per KV head, a BF16 or FP8-record pool, 16-byte aligned tiles (pool base and block
+// stride) and blocks below 2 GiB (its loads address a block through a buffer resource of 32-bit
+// size); anything else runs the generic kernel.
 bool fast_decode(const lk_decode_shape& s, const void* pool) {
     const uint32_t groups = s.query_heads / s.kv_heads;
     return s.slots == kSlots && s.head_dim == kDim && groups <= kMaxHeads && s.kv_format != LK_F32 && aligned(pool, 16) &&
-           pool_block_bytes(s) % 16 == 0;
+           pool_block_bytes(s) % 16 == 0 && pool_block_bytes(s) <= 0x7FFFFFFFull;
 }
 
 uint32_t compute_units();

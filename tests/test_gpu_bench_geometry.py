@@ -12,8 +12,10 @@ launches are the ones bench.py times:
 - the fused token write (lk_paged_decode_append) at 128- and 256-block splits and with more
   than 64 splits at 8 KV heads, BF16 and FP8, against the two-launch sequence and the oracle.
 - config 5: decode steps computed while 2,048 blocks swap out as FP8 records and back in equal
-  the same steps computed alone, bit for bit, and the swapped bytes equal the records of a
-  quiet quantize (themselves checked against the oracle on a sample).
+  the same steps computed alone, bit for bit; every swapped record equals the oracle's quantize
+  and every restored block its dequantize.
+- config 2: the 512-block FP8 swap of the 12 GiB pool through two 128 MiB slots, every record
+  and every restored block against the oracle.
 - a seeded randomized sweep of shapes, lengths, gains and dtypes, after the reference's
   property test (tests/test_triton_decode.py:335-353), and the reference's Qwen3-4B-shape
   case at layers 0, 17 and 35 (tests/test_triton_decode.py:649-684).
@@ -327,13 +329,89 @@ def test_fused_write_with_65_to_128_splits_at_8_kv_heads(hip_decode, fp8):
     assert_close(fused, expected, f"65 splits fp8={fp8}", rounding)
 
 
+def assert_swap_matches_the_oracle(pool, src, dst, payload, layout, chunk=128):
+    """Every record of a swap-out payload (host bytes, records in src order) against the
+    oracle's quantize of the source blocks, and every restored block (pool[dst]) against the
+    oracle's dequantize of those records, chunk by chunk, the oracle split over threads."""
+    record = layout.record_bytes
+    for start in range(0, len(src), chunk):
+        ids = src[start : start + chunk]
+        bits = pool[ids].view(torch.int16).cpu().numpy().view(np.uint16)
+        parts = [part for part in np.array_split(np.arange(len(ids)), ORACLE_THREADS) if len(part)]
+
+        def leg(part):
+            local = np.ascontiguousarray(bits[part])
+            local_ids = np.arange(len(part), dtype=np.int32)
+            records = oracle.quantize_records(local, local_ids, layout.group_elems, layout.groups_per_block)
+            restored = np.zeros_like(local)
+            oracle.dequantize_records(records, local_ids, restored, layout.group_elems, layout.groups_per_block)
+            return records, restored
+
+        with ThreadPoolExecutor(len(parts)) as workers:
+            legs = list(workers.map(leg, parts))
+        records = np.concatenate([r for r, _ in legs])
+        restored = np.concatenate([b for _, b in legs])
+        got = payload[start * record : (start + len(ids)) * record]
+        if not np.array_equal(got, records):
+            bad = np.flatnonzero(got != records)[0]
+            raise AssertionError(f"record {start + bad // record} (block {ids[bad // record]}) differs from the oracle at byte {bad % record}")
+        back = pool[dst[start : start + len(ids)]].view(torch.int16).cpu().numpy().view(np.uint16)
+        assert np.array_equal(back, restored), f"restored blocks {start}..{start + len(ids)} differ from the oracle's dequantize"
+
+
+def test_config2_swap_of_512_blocks_equals_the_oracle_record_for_record():
+    """BASELINE config 2 exactly: a 12 GiB Qwen3-4B pool (5,461 blocks) of N(0,1) BF16 with
+    0.1% of the elements at +/-40, 512 random non-contiguous blocks swapped out as FP8 records
+    through two 128 MiB staging slots (113 records each, so 5 segments) into pinned host
+    memory, then swapped in to 512 fresh random ids. All 512 records equal the oracle's
+    quantize of the source blocks, all 512 restored blocks equal the oracle's dequantize, and
+    every other block of the pool is unchanged (reference tests/test_fp8.py:264-278,
+    tests/test_transfer.py:546-569)."""
+    from layover_amd.config import ModelConfig
+    from layover_amd.kernels import fp8 as codec
+    from layover_amd.kv.paged_cache import PagedKVCache
+    from layover_amd.kv.transfer import NativeBackend
+
+    config = ModelConfig.qwen3_4b()
+    block_bytes = 2 * LAYERS * KV_HEADS * SLOTS * DIM * 2
+    blocks = (12 << 30) // block_bytes
+    assert blocks == 5461
+    cache = PagedKVCache(config, blocks, device="cuda", fill=False)
+    cache.pool.copy_(bf16_pool(blocks, seed=0, outliers=1e-3))
+    before = cache.pool.clone()
+    rng = np.random.default_rng(20)
+    picked = rng.permutation(blocks)
+    src, dst = [int(i) for i in picked[:512]], [int(i) for i in picked[512:1024]]
+    layout = codec.Fp8Layout(GROUP_ELEMS, GROUPS_PER_BLOCK)
+    backend = NativeBackend("cuda", staging_bytes=128 << 20, num_staging=2, ids_capacity=1 << 20)
+    try:
+        log("config 2: 512-block FP8 swap-out")
+        out_ticket = backend.start_out(cache, src, fp8=True)
+        out_ticket.wait()
+        payload = out_ticket.payload
+        host = payload.memory.numpy()[: 512 * layout.record_bytes].copy()
+        log("config 2: swap-in to 512 fresh ids")
+        backend.start_in(cache, dst, payload).wait()
+        torch.cuda.synchronize()
+        backend.free(payload)
+    finally:
+        backend.close()
+    log("config 2: all records and restored blocks against the oracle")
+    assert_swap_matches_the_oracle(cache.pool, src, dst, host, layout)
+    untouched = torch.ones(blocks, dtype=torch.bool, device="cuda")
+    untouched[torch.tensor(dst, device="cuda")] = False
+    assert torch.equal(cache.pool[untouched].view(torch.int16), before[untouched].view(torch.int16))
+    del cache, before
+    torch.cuda.empty_cache()
+
+
 def test_config5_decode_during_a_2048_block_fp8_swap_equals_decode_alone(hip_decode):
     """Config 5's overlap: batch-32 decode steps (36 layers each, mixed 1k-32k contexts) on
     torch's stream while 2,048 blocks swap out to pinned host memory as FP8 records on the
     backend's streams, then back in to fresh ids. Every overlapped step's outputs equal the
-    solo step's bit for bit; the payload equals a quiet quantize of the same blocks (checked
-    against the oracle on a sample); the restored blocks equal a quiet dequantize; and no
-    block outside the targets changes."""
+    solo step's bit for bit; the payload equals a quiet quantize of the same blocks and, all
+    2,048 records, the oracle's quantize; the restored blocks equal a quiet dequantize and the
+    oracle's dequantize; and no block outside the targets changes."""
     from layover_amd.config import ModelConfig
     from layover_amd.kernels import fp8 as codec
     from layover_amd.kv.paged_cache import PagedKVCache
@@ -365,11 +443,6 @@ def test_config5_decode_during_a_2048_block_fp8_swap_equals_decode_alone(hip_dec
     expected_pool = cache.pool.clone()
     codec.dequantize_blocks(quiet, torch.tensor(dst, dtype=torch.int32, device="cuda"), expected_pool, layout)
     torch.cuda.synchronize()
-    sample = [0, 777, swap_blocks - 1]
-    bits = cache.pool[[src[i] for i in sample]].view(torch.int16).cpu().numpy().view(np.uint16)
-    oracle_records = oracle.quantize_records(bits, range(len(sample)), GROUP_ELEMS, GROUPS_PER_BLOCK)
-    quiet_rows = quiet.view(swap_blocks, -1)
-    assert np.array_equal(quiet_rows[sample].cpu().numpy().reshape(-1), oracle_records)
 
     backend = NativeBackend("cuda", staging_bytes=128 << 20, num_staging=2, ids_capacity=1 << 20)
     try:
@@ -402,6 +475,8 @@ def test_config5_decode_during_a_2048_block_fp8_swap_equals_decode_alone(hip_dec
         log(f"config 5: {len(overlapped)} decode steps overlapped the swap")
         assert np.array_equal(host, quiet.cpu().numpy())
         assert torch.equal(cache.pool.view(torch.int16), expected_pool.view(torch.int16))
+        log("config 5: all 2,048 swapped records and restored blocks against the oracle")
+        assert_swap_matches_the_oracle(cache.pool, src, dst, host, layout)
         for i, got in enumerate(overlapped):
             assert torch.equal(got.view(torch.int16), solo.view(torch.int16)), f"overlapped step {i} differs from the solo step"
         assert in_ticket.done()
