@@ -200,8 +200,12 @@ int lk_paged_decode_append(const lk_decode_shape* shape, const void* q, void* po
  * arguments minus the workspace, whose split partials go to a file-scope device array of
  * 16 MiB per GPU (held until the process ends; its address is looked up on the first call
  * on each device). A shape whose lk_paged_decode_workspace exceeds 16 MiB is refused with
- * LK_ERR_INVALID. Calls on one GPU share the array: calls that overlap on one GPU race.
- * It calls no hipMalloc or hipFree. */
+ * LK_ERR_INVALID. Calls on one GPU share the array, so they are ordered: a call on a stream
+ * other than the previous call's first makes its stream wait for that call (an event recorded
+ * after each call; one event per device, created on the first call). Under HIP graph capture
+ * no event is used: captured calls are ordered by their graph, and replays of graphs holding
+ * such calls must not overlap on one GPU. The stream must belong to the current device
+ * (LK_ERR_INVALID otherwise). It calls no hipMalloc or hipFree. */
 int lk_paged_decode_static(const lk_decode_shape* shape, const void* q, const void* pool, const int32_t* table,
                            const int32_t* lengths, void* out, void* stream);
 

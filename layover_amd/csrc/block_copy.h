@@ -62,13 +62,26 @@ inline uint64_t chunks_for(uint64_t block_bytes, bool wide_words) {
     return (block_bytes + chunk - 1) / chunk;
 }
 
+// A launch moves at most this many chunks: a dispatch holds fewer than 2^32 work-items, one
+// 64-lane workgroup per chunk.
+constexpr uint64_t kMaxChunks = 0xFFFFFFFFull / kLanes;
+
+// Whether `blocks` blocks of `block_bytes` fit one launch with either word size (the 8-byte
+// count bounds both).
+inline bool launch_fits(uint64_t block_bytes, uint64_t blocks) {
+    const uint64_t chunks = chunks_for(block_bytes, false);
+    return blocks == 0 || (chunks <= kMaxChunks && chunks * blocks <= kMaxChunks);
+}
+
 // Launch helpers: `blocks` blocks of `block_bytes` (a multiple of 8; pool and staging 8-byte
-// aligned), ids[i] naming the pool block of staging slot i. The caller checks the arguments.
+// aligned), ids[i] naming the pool block of staging slot i. The caller checks the arguments
+// (launch_fits among them); a grid beyond one dispatch is refused here too.
 inline hipError_t launch_gather(hipStream_t stream, const uint8_t* pool, const uint32_t* ids, uint8_t* staging, uint64_t block_bytes,
                                 uint32_t blocks) {
     const bool w16 = wide(pool, staging, block_bytes);
+    if (!launch_fits(block_bytes, blocks)) return hipErrorInvalidValue;
     const uint32_t chunks = uint32_t(chunks_for(block_bytes, w16));
-    const dim3 grid(chunks * blocks);
+    const dim3 grid(uint32_t(uint64_t(chunks) * blocks));
     if (w16)
         hipLaunchKernelGGL(gather_blocks<Word16>, grid, dim3(kLanes), 0, stream, pool, ids, staging, block_bytes, chunks);
     else
@@ -79,8 +92,9 @@ inline hipError_t launch_gather(hipStream_t stream, const uint8_t* pool, const u
 inline hipError_t launch_scatter(hipStream_t stream, uint8_t* pool, const uint32_t* ids, const uint8_t* staging, uint64_t block_bytes,
                                  uint32_t blocks) {
     const bool w16 = wide(pool, staging, block_bytes);
+    if (!launch_fits(block_bytes, blocks)) return hipErrorInvalidValue;
     const uint32_t chunks = uint32_t(chunks_for(block_bytes, w16));
-    const dim3 grid(chunks * blocks);
+    const dim3 grid(uint32_t(uint64_t(chunks) * blocks));
     if (w16)
         hipLaunchKernelGGL(scatter_blocks<Word16>, grid, dim3(kLanes), 0, stream, pool, ids, staging, block_bytes, chunks);
     else

@@ -188,6 +188,9 @@ class HostDevice {
     void memcpy_to_host(Stream stream, void* dst, const void* src, uint64_t bytes) { push_copy(stream, dst, src, bytes); }
     void memcpy_to_device(Stream stream, void* dst, const void* src, uint64_t bytes) { push_copy(stream, dst, src, bytes); }
 
+    // Host copies have no per-launch size limit.
+    bool launch_fits(uint64_t, uint64_t) const { return true; }
+
     // Block copies in the order of ids: block i of the staging buffer is pool block ids[i].
     void launch_gather(Stream stream, const uint8_t* pool, const uint32_t* ids, uint8_t* staging, uint64_t block_bytes, uint32_t blocks) {
         stream->push([=] {

@@ -630,9 +630,16 @@ LK_EXPORT int lk_paged_decode_append(const lk_decode_shape* shape, const void* q
 // lk_paged_decode_static: lk_paged_decode with its split partials in a file-scope device array
 // instead of a caller's workspace, for callers that cannot allocate. The array's address is
 // looked up once per device (hipGetSymbolAddress, with that device current) and kept; the
-// host-side name `decode_scratch` is only a stand-in and never reaches a kernel. Calls on one
-// device share the array and must not overlap; nothing in it needs clearing between calls
-// (the merge reads only the splits a row's length covers, all written by the same launch).
+// host-side name `decode_scratch` is only a stand-in and never reaches a kernel. Nothing in it
+// needs clearing between calls (the merge reads only the splits a row's length covers, all
+// written by the same launch).
+//
+// Calls on one device share the array, so they are ordered: each call records an event on its
+// stream after its launches, and a call on another stream first makes its stream wait for that
+// event, so a launch never overwrites partials that another stream's merge has yet to read.
+// Under HIP graph capture (either call's stream capturing) events are left alone: a captured
+// call's order is the graph's, and replays on different streams must not overlap (the
+// caller's rule). The stream must belong to the current device, whose array is used.
 namespace lk {
 
 constexpr uint64_t kStaticScratchBytes = 16ull << 20;
@@ -640,21 +647,45 @@ constexpr int kMaxDevices = 64;
 
 static __device__ __align__(256) uint8_t decode_scratch[kStaticScratchBytes];
 
-std::mutex scratch_lock;
-void* scratch_address[kMaxDevices] = {};
+struct StaticScratch {
+    void* address = nullptr;
+    hipEvent_t done = nullptr;       // recorded after the last uncaptured call's launches
+    hipStream_t stream = nullptr;    // that call's stream
+    bool recorded = false;
+};
+std::mutex scratch_lock;  // held from the lookup to the event record, so calls from two threads are ordered too
+StaticScratch scratch_state[kMaxDevices];
 
-void* device_scratch() {
+void run_decode_static(const lk_decode_shape& s, const void* q, const void* pool, const int32_t* table, const int32_t* lengths, void* out,
+                       hipStream_t stream) {
     int device = -1;
     require(hipGetDevice(&device) == hipSuccess && device >= 0 && device < kMaxDevices, "no usable current HIP device");
+    int stream_device = device;
+    if (stream != nullptr) require(hipStreamGetDevice(stream, &stream_device) == hipSuccess, "hipStreamGetDevice failed on the stream");
+    if (stream_device != device)
+        throw Invalid("the stream belongs to device " + std::to_string(stream_device) + ", the current device is " + std::to_string(device) +
+                      ": make the stream's device current");
+    hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+    require(hipStreamIsCapturing(stream, &capture) == hipSuccess, "hipStreamIsCapturing failed");
+    const bool captured = capture != hipStreamCaptureStatusNone;
     std::lock_guard<std::mutex> hold(scratch_lock);
-    if (scratch_address[device] == nullptr) {
+    StaticScratch& state = scratch_state[device];
+    if (state.address == nullptr) {
         void* address = nullptr;
         const hipError_t status = hipGetSymbolAddress(&address, HIP_SYMBOL(decode_scratch));
         if (status != hipSuccess || address == nullptr)
             throw std::runtime_error(std::string("hipGetSymbolAddress(decode_scratch): ") + hipGetErrorString(status));
-        scratch_address[device] = address;
+        state.address = address;
     }
-    return scratch_address[device];
+    if (state.done == nullptr) require(hipEventCreateWithFlags(&state.done, hipEventDisableTiming) == hipSuccess, "hipEventCreate failed");
+    if (!captured && state.recorded && state.stream != stream)
+        require(hipStreamWaitEvent(stream, state.done, 0) == hipSuccess, "hipStreamWaitEvent on the previous static call failed");
+    run_decode(s, q, pool, table, lengths, out, state.address, kStaticScratchBytes, nullptr, stream);
+    if (!captured) {
+        require(hipEventRecord(state.done, stream) == hipSuccess, "hipEventRecord after the static call failed");
+        state.stream = stream;
+        state.recorded = true;
+    }
 }
 
 }  // namespace lk
@@ -668,8 +699,7 @@ LK_EXPORT int lk_paged_decode_static(const lk_decode_shape* shape, const void* q
         if (need > lk::kStaticScratchBytes)
             throw lk::Invalid("lk_paged_decode_static: this shape needs " + std::to_string(need) + " bytes of split partials, above the " +
                               std::to_string(lk::kStaticScratchBytes) + "-byte static scratch; use lk_paged_decode with a workspace");
-        lk::run_decode(*shape, q, pool, table, lengths, out, lk::device_scratch(), lk::kStaticScratchBytes, nullptr,
-                       static_cast<hipStream_t>(stream));
+        lk::run_decode_static(*shape, q, pool, table, lengths, out, static_cast<hipStream_t>(stream));
     });
 }
 
@@ -910,7 +940,7 @@ void check_block_copy(const void* pool, const uint32_t* ids, uint32_t count, uin
     require(count == 0 || (pool != nullptr && staging != nullptr && ids != nullptr), "null pool, ids or staging");
     require(block_bytes > 0 && block_bytes % 8 == 0 && aligned(pool, 8) && aligned(staging, 8),
             "pool and staging must be 8-byte aligned and block_bytes a positive multiple of 8");
-    require(blockcopy::chunks_for(block_bytes, false) * count <= 0x7FFFFFFFull, "too many chunks for one launch");
+    require(blockcopy::launch_fits(block_bytes, count), "too many chunks for one launch (at most 2^32 / 64 chunks of 512 bytes)");
 }
 
 }  // namespace lk

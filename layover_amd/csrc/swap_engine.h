@@ -348,10 +348,21 @@ class SwapEngine {
             misuse("pool and host must be 8-byte aligned and block_bytes a multiple of 8");
         if (block_bytes > staging_bytes_) misuse("one block is larger than a staging buffer");
         if (count > ids_capacity_) misuse("transfer has more blocks than ids_capacity");
+        const uint64_t per_segment = std::min<uint64_t>(staging_bytes_ / block_bytes, kMaxSegmentBlocks);
+        if (!dev_.launch_fits(block_bytes, per_segment)) misuse("a staging buffer of these blocks is too many chunks for one kernel launch");
         prepare_staging();
         Ticket* ticket = new_ticket();
-        const uint32_t* device_ids = count ? upload_ids(ids, count, ticket) : nullptr;
-        const uint64_t per_segment = std::min<uint64_t>(staging_bytes_ / block_bytes, kMaxSegmentBlocks);
+        const uint32_t* device_ids = nullptr;
+        if (count) {
+            // A transfer whose ids never reached the device was never started: its ticket goes
+            // (it was not handed out), so it neither lingers nor counts as a transfer.
+            try {
+                device_ids = upload_ids(ids, count, ticket);
+            } catch (...) {
+                if (!ticket->owns_ids) drop_ticket(ticket);
+                throw;
+            }
+        }
         const bool out = direction == Direction::ToHost;
         Stream fill_on = out ? compute_ : copy_;
         Stream drain_on = out ? copy_ : compute_;
@@ -525,6 +536,12 @@ class SwapEngine {
         tickets_.emplace(raw, std::move(ticket));
         stats_.transfers++;
         return raw;
+    }
+
+    void drop_ticket(Ticket* ticket) {
+        quietly([&] { dev_.event_destroy(ticket->done); });
+        tickets_.erase(ticket);
+        stats_.transfers--;
     }
 
     void live(Ticket* ticket) const {

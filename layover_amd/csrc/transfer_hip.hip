@@ -111,6 +111,8 @@ class HipDevice {
         check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream), "hipMemcpyAsync(host to device)");
     }
 
+    bool launch_fits(uint64_t block_bytes, uint64_t blocks) const { return blockcopy::launch_fits(block_bytes, blocks); }
+
     void launch_gather(Stream stream, const uint8_t* pool, const uint32_t* ids, uint8_t* staging, uint64_t block_bytes, uint32_t blocks) {
         check(blockcopy::launch_gather(stream, pool, ids, staging, block_bytes, blocks), "launch gather_blocks");
     }

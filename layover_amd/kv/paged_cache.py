@@ -5,9 +5,9 @@ Pool layout [block, kind, layer, kv_head, slot, dim], kind 0 = K and 1 = V
 and its FP8 record's groups are (kind, layer, kv_head) in pool order. decode_rows builds the
 reference's decode table rows (paged_cache.py:154-169).
 
-A sequence's BlockTable lists its blocks in token order; blocks are reference counted by the
-allocator, so tables can share a prefix (fork) and a shared block is copied before it is
-written (make_writable, prepare_write), as in paged_cache.py:58-101.
+A sequence's BlockTable lists its blocks in token order. Growing, sharing and releasing
+tables (the reference's paged_cache.py:58-101) belong to the engine's scheduler, outside this
+data path; callers build tables from the allocator's ids.
 """
 
 from __future__ import annotations
@@ -72,56 +72,6 @@ class PagedKVCache:
     def blocks_for(self, tokens: int) -> int:
         return -(-tokens // self.block_tokens)
 
-    # -- a sequence's blocks (paged_cache.py:58-101) --
-
-    def ensure_capacity(self, table: BlockTable, tokens: int) -> None:
-        """Append newly allocated blocks until the table can hold `tokens` tokens."""
-        short = self.blocks_for(tokens) - len(table.blocks)
-        if short > 0:
-            table.blocks += self.allocator.alloc(short)
-
-    def make_writable(self, table: BlockTable, index: int) -> None:
-        """Copy-on-write for the table's block `index`: if another table also holds it, this
-        table gets a fresh block with the same contents and lets go of the shared one."""
-        shared = table.blocks[index]
-        if self.allocator.refcount(shared) < 2:
-            return
-        (private,) = self.allocator.alloc(1)
-        self.pool[private].copy_(self.pool[shared])
-        self.allocator.decref(shared)
-        table.blocks[index] = private
-
-    def prepare_write(self, table: BlockTable, start: int, end: int) -> None:
-        """Make tokens [start, end) writable: grow the table to hold them, give it private
-        copies of the blocks they fall in, and extend its length to `end` if shorter."""
-        self.ensure_capacity(table, end)
-        for index in range(start // self.block_tokens, self.blocks_for(end)):
-            self.make_writable(table, index)
-        table.num_tokens = max(table.num_tokens, end)
-
-    def fork(self, table: BlockTable, tokens: int | None = None) -> BlockTable:
-        """A new table sharing the blocks that hold the first `tokens` tokens (default all of
-        them); each shared block gains a reference."""
-        tokens = table.num_tokens if tokens is None else tokens
-        if tokens > table.num_tokens:
-            raise ValueError(f"cannot fork {tokens} tokens from a table of {table.num_tokens}")
-        prefix = table.blocks[: self.blocks_for(tokens)]
-        for block in prefix:
-            self.allocator.incref(block)
-        return BlockTable(list(prefix), tokens)
-
-    def truncate(self, table: BlockTable, tokens: int) -> None:
-        """Keep the first `tokens` tokens; blocks past them lose this table's reference."""
-        keep = self.blocks_for(tokens)
-        dropped, table.blocks = table.blocks[keep:], table.blocks[:keep]
-        for block in dropped:
-            self.allocator.decref(block)
-        table.num_tokens = min(table.num_tokens, tokens)
-
-    def release(self, table: BlockTable) -> None:
-        """Drop all of the table's blocks; it is left empty."""
-        self.truncate(table, 0)
-
     def _upload(self, values) -> torch.Tensor:
         """Host values to the pool's device as one copy. On a GPU it goes through pinned memory
         so that it is queued behind work already launched instead of waiting for it
@@ -168,7 +118,7 @@ class PagedKVCache:
 
     def write_range(self, table: BlockTable, layer: int, start: int, k: torch.Tensor, v: torch.Tensor) -> None:
         """k and v, [kv_heads, count, head_dim], stored at tokens [start, start + count) of the
-        table (paged_cache.py:130-136); the table must have been through prepare_write."""
+        table (paged_cache.py:130-136); the table must already list those tokens' blocks."""
         _, blocks, slots = self.chunk_locations(table, start, k.shape[1])
         self.write_at(blocks, slots, layer, k, v)
 

@@ -109,3 +109,18 @@ def test_headers_are_plain_c(tmp_path):
                              f"-I{ROOT / 'include'}", str(source)], capture_output=True, text=True)
     assert result.returncode == 0, result.stderr
 
+
+
+def test_block_copies_beyond_one_dispatch_are_refused_without_launching():
+    """A gather or scatter of more 512-byte chunks than one dispatch's 2^32 work-items hold
+    (64 lanes per chunk) is refused with LK_ERR_INVALID before anything touches memory."""
+    kernels = _lib.load()
+    word = ctypes.c_uint64(0)
+    ptr = ctypes.addressof(word)
+    block_bytes = 1 << 20  # 2,048 chunks of 512 bytes
+    limit = (2**32 - 1) // 64 // 2048  # blocks per launch
+    for function in (kernels.lk_gather_blocks, kernels.lk_scatter_blocks):
+        assert function(ptr, ptr, limit + 1, block_bytes, ptr, None) == _lib.LK_ERR_INVALID
+        assert b"too many chunks" in kernels.lk_last_error()
+    assert kernels.lk_gather_blocks(ptr, ptr, 1, 2**40, ptr, None) == _lib.LK_ERR_INVALID
+

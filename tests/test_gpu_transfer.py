@@ -231,3 +231,26 @@ def test_cpu_tier_offload_and_prefix_restore_on_the_gpu(fp8):
         assert np.array_equal(after, reference)
     finally:
         backend.close()
+
+
+def test_staging_too_large_for_one_block_copy_launch_is_a_caller_error():
+    """A staging buffer holding more 512-byte chunks of a block than one block-copy dispatch
+    moves (2^32 work-items, 64 lanes per chunk) is refused with LT_ERR_INVALID, a caller error
+    that leaves the engine usable, before any staging is allocated (64 GiB are asked for and
+    never allocated): no transfer or kernel is counted."""
+    from layover_amd.kv.native import LT_ERR_INVALID, Engine, NativeError
+
+    torch.cuda.synchronize()
+    engine = Engine("hip", staging_bytes=64 << 30, ids_capacity=64)
+    try:
+        block = 2_359_296
+        pool = torch.zeros(2 * block, dtype=torch.uint8, device="cuda")
+        host = engine.host_alloc(block)
+        with pytest.raises(NativeError) as refused:
+            engine.out_gather(pool.data_ptr(), block, [1], host)
+        assert refused.value.status == LT_ERR_INVALID and "too many chunks" in str(refused.value)
+        stats = engine.stats()
+        assert stats["transfers"] == 0 and stats["kernels"] == 0, stats
+        engine.host_free(host)
+    finally:
+        engine.destroy()

@@ -85,3 +85,57 @@ def test_a_shape_beyond_the_static_scratch_is_refused_before_launch():
                                         dummy.data_ptr(), _lib.current_stream(dummy.device))
     assert status == _lib.LK_ERR_INVALID
     assert b"static scratch" in lib.lk_last_error()
+
+
+def test_static_calls_on_two_streams_are_ordered_and_equal_the_workspace_decode():
+    """Calls alternating between two streams share the one array; each call's stream waits for
+    the previous call, so every output equals its workspace decode bit for bit, the case with
+    the most splits (batch 32 up to 32,768 tokens) followed by a small one on the other stream,
+    in a row with no synchronization between them."""
+    from layover_amd.kernels import _lib, hip_decode
+
+    lib = _lib.load()
+    print("no-alloc decode on two streams", flush=True)
+    cases = [case(32, 32768, seed=5), case(3, 700, seed=6), case(16, 8000, seed=7)]
+    expected = [run_both(c[0], c[1], c[3], c[4], layer=2)[0] for c in cases]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = [torch.full_like(c[0], float("nan")) for c in cases]
+    torch.cuda.synchronize()
+    for round_ in range(3):
+        for i, (q, target, _, table, lengths) in enumerate(cases):
+            stream = streams[(i + round_) % 2]
+            shape = hip_decode.decode_shape(q, target, 2, table, 4, lengths)
+            _lib.check(lib.lk_paged_decode_static(shape, q.data_ptr(), target.data_ptr(), table.data_ptr(), lengths.data_ptr(),
+                                                  outs[i].data_ptr(), stream.cuda_stream))
+        torch.cuda.synchronize()
+        for i in range(len(cases)):
+            assert torch.equal(outs[i].view(torch.int16), expected[i].view(torch.int16)), f"round {round_}, case {i}"
+            outs[i].fill_(float("nan"))
+
+
+def test_static_decode_captured_in_a_graph_replays_like_the_eager_call():
+    """The entry point under HIP graph capture (the callers it is for): replays, with eager work
+    and synchronizations between them, each equal the workspace decode bit for bit."""
+    from layover_amd.kernels import _lib, hip_decode
+
+    lib = _lib.load()
+    print("no-alloc decode under graph capture", flush=True)
+    q, target, _, table, lengths = case(8, 4096, seed=8)
+    expected = run_both(q, target, table, lengths, layer=0)[0]
+    shape = hip_decode.decode_shape(q, target, 0, table, 4, lengths)
+    out = torch.full_like(q, float("nan"))
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            _lib.check(lib.lk_paged_decode_static(shape, q.data_ptr(), target.data_ptr(), table.data_ptr(), lengths.data_ptr(),
+                                                  out.data_ptr(), side.cuda_stream))
+    torch.cuda.synchronize()
+    other = case(3, 700, seed=9)
+    for replay in range(3):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), expected.view(torch.int16)), f"replay {replay}"
+        run_both(other[0], other[1], other[3], other[4], layer=1)  # eager static call between replays
