@@ -960,6 +960,7 @@ def main() -> None:
     parser.add_argument("--skip-graphs", action="store_true", help="skip the HIP-graph decode steps (rocprofv3 --pmc cannot follow replays)")
     parser.add_argument("--decode-scan", action="store_true", help="run only the batch-1 decode scan over context lengths and print it")
     parser.add_argument("--duplex", action="store_true", help="run only the concurrent swap-out + swap-in measurement and print it")
+    parser.add_argument("--overlap-only", action="store_true", help="run only config 5 (decode beside a 2,048-block FP8 swap) and print it")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this KV data path has no multi-GPU step (--gpus {args.gpus} refused)", file=sys.stderr)
@@ -989,6 +990,10 @@ def main() -> None:
     cache = PagedKVCache(config, pool_blocks, device=device, fill=False)
     fill_pool(cache.pool, seed=0, outlier_fraction=0.001)
     torch.cuda.synchronize()
+    if args.overlap_only:
+        log("overlap: decode during a 2,048-block FP8 swap (config 5)")
+        print(json.dumps({"overlap": overlap_bench(device, cache, pool_blocks)}), flush=True)
+        return
 
     log("link probe")
     link = measure_link(device)

@@ -20,5 +20,5 @@ def test_more_than_one_gpu_is_refused_with_a_message():
 
 def test_the_separate_modes_are_offered():
     text = run_bench("--help").stdout
-    for flag in ("--steps", "--warmup", "--decode-scan", "--duplex", "--skip-cpu"):
+    for flag in ("--steps", "--warmup", "--decode-scan", "--duplex", "--overlap-only", "--skip-cpu"):
         assert flag in text
