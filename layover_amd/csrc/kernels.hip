@@ -870,6 +870,7 @@ void run_prefill(const lk_prefill_shape& s, const void* q, const void* pool, con
     a.scale_log2 = s.scale * kLog2e;
     a.key_splits = p.key_splits;
     a.split_steps = p.split_steps;
+    a.paired = grid <= 2ull * compute_units() ? 1u : 0u;
     uint8_t* const space = static_cast<uint8_t*>(workspace);
     a.partial_acc = p.key_splits > 1 ? reinterpret_cast<float*>(space + parts.stage_bytes + parts.index_bytes) : nullptr;
     a.partial_ml = p.key_splits > 1 ? a.partial_acc + uint64_t(s.kv_heads) * rows * p.key_splits * kDim : nullptr;

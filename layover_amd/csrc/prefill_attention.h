@@ -44,6 +44,12 @@ struct PrefillArgs {
     // instead of out; prefill_merge then combines them.
     uint32_t key_splits;       // 1: no split, results straight to out
     uint32_t split_steps;
+    // Tile order of the LDS kernel. 0: heaviest first (causal tiles grow with their index), for
+    // grids that run in several rounds. 1: the grid is resident at once (at most two
+    // workgroups per CU): the first half of the order heaviest first, the second half lightest
+    // first, so that the two workgroups that share a CU (w and w + half the grid, dealt
+    // alike) carry about equal work together.
+    uint32_t paired;
     float* partial_acc;
     float* partial_ml;
 };
@@ -364,10 +370,14 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
     const uint32_t g = lane / 16;
     const uint32_t n = lane % 16;
     // KV head fastest (a head's workgroups stay on one XCD), then the splits of a tile, then
-    // the tiles, heaviest first.
+    // the tiles, heaviest first, or paired (see PrefillArgs::paired). Measured on MI355X,
+    // 2,048-token chunk at position 0 (512 workgroups, two per CU): 62.7 -> 57.4 us per layer
+    // paired; chunks of 1,024 and 4,096 tokens unchanged.
     const uint32_t kv_head = blockIdx.x % a.kv_heads;
     const uint32_t split = (blockIdx.x / a.kv_heads) % a.key_splits;
-    const uint32_t tile = a.row_tiles - 1 - blockIdx.x / (a.kv_heads * a.key_splits);
+    const uint32_t order = blockIdx.x / (a.kv_heads * a.key_splits);
+    const uint32_t half = (a.row_tiles + 1) / 2;
+    const uint32_t tile = a.paired && order >= half ? order - half : a.row_tiles - 1 - order;
     const uint32_t total_rows = a.tokens * a.groups;
     const uint32_t wg_row0 = tile * kLdsWaves * kLdsRows;
     const uint32_t row0 = wg_row0 + wave * kLdsRows;
