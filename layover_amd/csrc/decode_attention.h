@@ -263,7 +263,7 @@ __device__ __forceinline__ bool decode_unit_of(const DecodeArgs& a, uint32_t w, 
 // the FP8 kernel went from 170 to 152 us per layer at batch 32 (0.79 -> 0.89 of 8 TB/s) and
 // from 84.5 to 76 us at batch 64 @ 4,096 (measured on MI355X, A/B in one process). For BF16
 // pools the same request, or three or four waves with a one-tile ring, measured no faster.
-template <int KV, int QF, int kWaves, bool kStream>
+template <int KV, int QF, int kWaves, bool kStream, bool kAppend>
 __global__ __launch_bounds__(kWave* kWaves) __attribute__((amdgpu_waves_per_eu(KV == LK_FP8_RECORD ? 2 : 1))) void decode_split_mfma(
     DecodeArgs a) {
     constexpr uint32_t kDecodeWaves = kWaves;
@@ -328,7 +328,7 @@ __global__ __launch_bounds__(kWave* kWaves) __attribute__((amdgpu_waves_per_eu(K
     // the output written here (one split; 8-wave kernels only, which small grids run), a row
     // of no tokens still writes it (NaN, as the combine would).
     const uint32_t nblocks = blocks_of(length, kSlots);
-    constexpr bool kMayWriteOut = kWaves == 8;
+    constexpr bool kMayWriteOut = kWaves >= 8;
     const bool writes_out = kMayWriteOut && a.out != nullptr;
     if (first >= nblocks && !writes_out) return;
     const uint32_t count = min(a.bps, nblocks - first);
@@ -347,7 +347,7 @@ __global__ __launch_bounds__(kWave* kWaves) __attribute__((amdgpu_waves_per_eu(K
     // fetched as usual and the written slot's rows replaced by the new token (which is what
     // memory holds once the write lands); FP8 groups are re-encoded whole, and the new codes go
     // to LDS, where the same wave reads them back in the tile's layout, with the new shifts.
-    const bool writes = a.write_block != nullptr && count > 0 && first + count == nblocks;
+    const bool writes = kAppend && a.write_block != nullptr && count > 0 && first + count == nblocks;
     const uint32_t writer = writes ? (count - 1) % kDecodeWaves : kDecodeWaves;
     constexpr bool kBf16 = KV == LK_BF16;
     uint32_t patch_k[kBf16 ? 16 : 1] = {}, patch_v[kBf16 ? 4 : 1] = {};
@@ -360,7 +360,7 @@ __global__ __launch_bounds__(kWave* kWaves) __attribute__((amdgpu_waves_per_eu(K
     // With 8 waves (small grids) the writer issues its first tile loads before re-encoding, so
     // the two sets of loads are in flight together; the 4-wave kernel re-encodes at once, which
     // keeps the loaded values out of its main loop's registers (three waves per SIMD for FP8).
-    constexpr bool kLateEncode = !kBf16 && kWaves == 8;
+    constexpr bool kLateEncode = !kBf16 && kWaves >= 8;
     // FP8: the two re-encodes, their codes also to LDS for the written unit's consume.
     auto reencode = [&]() __attribute__((always_inline)) {
         if constexpr (!kBf16) {
@@ -683,7 +683,7 @@ __global__ __launch_bounds__(kWave* kWaves) __attribute__((amdgpu_waves_per_eu(K
 #ifndef LK_DECODE_RING8_FP8
 #define LK_DECODE_RING8_FP8 LK_DECODE_RING_FP8
 #endif
-    constexpr int kRing = kWaves == 8 ? (KV == LK_BF16 ? LK_DECODE_RING8_BF16 : LK_DECODE_RING8_FP8)
+    constexpr int kRing = kWaves >= 8 ? (KV == LK_BF16 ? LK_DECODE_RING8_BF16 : LK_DECODE_RING8_FP8)
                                       : (KV == LK_BF16 ? LK_DECODE_RING_BF16 : LK_DECODE_RING_FP8);
     MfmaTile<KV> ring[kRing];
     if (mine > 0) {
@@ -936,6 +936,76 @@ __device__ __forceinline__ void combine_dim128(const DecodeArgs& a, void* out, u
 template <int QF, bool kTwoPages>
 __global__ __launch_bounds__(kWave) void decode_combine_vector(DecodeArgs a, void* out) {
     combine_dim128<QF, kTwoPages>(a, out, blockIdx.x / a.query_heads, blockIdx.x % a.query_heads);
+}
+
+// Combine for 128-dim heads spread over four workgroups per (sequence, query head), one per
+// quarter of the dims: lane l takes dims 32 q + 4 (l % 8) .. +3 of splits l / 8, l / 8 + 8, ...
+// A lane loads a quarter of the rows combine_dim128 does (4 rather than 32 at 32 splits), so
+// the one round trip to memory that the merge costs ends sooner.
+template <int QF, bool kTwoPages>
+__global__ __launch_bounds__(kWave) void decode_combine_quarter(DecodeArgs a, void* out) {
+    constexpr uint32_t kPages = kTwoPages ? 2 : 1;
+    constexpr uint32_t kGroups = 8, kRows = kPages * kWave / kGroups;
+    const uint32_t lane = threadIdx.x, col = lane % kGroups, grp = lane / kGroups;
+    const uint32_t quarter = blockIdx.x % 4, pair = blockIdx.x / 4;
+    const uint32_t seq = pair / a.query_heads, qh = pair % a.query_heads;
+    const int32_t length = a.lengths[uint64_t(seq) * a.lengths_stride];
+    const uint64_t base = (uint64_t(seq) * a.query_heads + qh) * a.splits;
+    const float* ml = a.partial_ml + 2 * base;
+    const f32x4* acc = reinterpret_cast<const f32x4*>(a.partial_acc + base * kDim) + quarter * 8 + col;
+    float lane_m[kPages], lane_l[kPages];
+#pragma unroll
+    for (uint32_t page = 0; page < kPages; ++page) {
+        lane_m[page] = -INFINITY;
+        lane_l[page] = 0.0f;
+        if (page * kWave + lane < a.splits) {
+            lane_m[page] = ml[2 * (page * kWave + lane)];
+            lane_l[page] = ml[2 * (page * kWave + lane) + 1];
+        }
+    }
+    f32x4 rows[kRows];
+#pragma unroll
+    for (uint32_t j = 0; j < kRows; ++j) {
+        const uint32_t s = grp + kGroups * j;
+        if (s < a.splits) rows[j] = acc[uint64_t(s) * (kDim / 4)];
+    }
+    const uint32_t used = (blocks_of(length, a.slots) + a.bps - 1) / a.bps;
+    float top = -INFINITY;
+#pragma unroll
+    for (uint32_t page = 0; page < kPages; ++page) top = page * kWave + lane < used ? fmaxf(top, lane_m[page]) : top;
+#pragma unroll
+    for (int mask = 32; mask >= 1; mask >>= 1) top = fmaxf(top, __shfl_xor(top, mask, kWave));
+    float weight[kPages], total = 0.0f;
+#pragma unroll
+    for (uint32_t page = 0; page < kPages; ++page) {
+        weight[page] = page * kWave + lane < used ? merge_weight(lane_m[page], top) : 0.0f;
+        total += page * kWave + lane < used ? lane_l[page] * weight[page] : 0.0f;
+    }
+#pragma unroll
+    for (int mask = 32; mask >= 1; mask >>= 1) total += __shfl_xor(total, mask, kWave);
+    f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (uint32_t j = 0; j < kRows; ++j) {
+        const uint32_t s = grp + kGroups * j;
+        const float w = __shfl(weight[j * kGroups / kWave], int(s % kWave), kWave);
+        // Splits past the used ones hold anything: selected away, never multiplied by zero.
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sum[i] = s < used ? fmaf(w, rows[j][i], sum[i]) : sum[i];
+    }
+#pragma unroll
+    for (int mask = kGroups; mask < int(kWave); mask <<= 1)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sum[i] += __shfl_xor(sum[i], mask, kWave);
+    if (grp != 0) return;
+    const float inverse = 1.0f / total;
+    const uint64_t at = (uint64_t(seq) * a.query_heads + qh) * kDim + 32 * quarter + 4 * col;
+    if constexpr (QF == LK_BF16) {
+        const uint32_t lo = uint32_t(to_bf16(sum[0] * inverse)) | (uint32_t(to_bf16(sum[1] * inverse)) << 16);
+        const uint32_t hi = uint32_t(to_bf16(sum[2] * inverse)) | (uint32_t(to_bf16(sum[3] * inverse)) << 16);
+        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(out) + at) = u32x2{lo, hi};
+    } else {
+        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(out) + at) = f32x4{sum[0] * inverse, sum[1] * inverse, sum[2] * inverse, sum[3] * inverse};
+    }
 }
 
 __host__ inline bool vector_combine_fits(const DecodeArgs& a) { return a.vector_combine && a.head_dim == kDim && a.splits <= kVectorSplits; }

@@ -209,18 +209,32 @@ uint32_t decode_waves(const DecodeArgs& a, uint64_t grid) {
     return a.groups <= 8 ? 8 : 4;
 }
 
+template <int KV, int QF, bool kAppend>
+void launch_split_mfma_as(const DecodeArgs& a, uint32_t waves, uint32_t grid, hipStream_t stream) {
+    const dim3 block(kWave * waves);
+    if (a.shared_blocks) {
+        if (waves == 8) hipLaunchKernelGGL((decode_split_mfma<KV, QF, 8, false, kAppend>), dim3(grid), block, 0, stream, a);
+        else hipLaunchKernelGGL((decode_split_mfma<KV, QF, 4, false, kAppend>), dim3(grid), block, 0, stream, a);
+    } else {
+        if (waves == 8) hipLaunchKernelGGL((decode_split_mfma<KV, QF, 8, true, kAppend>), dim3(grid), block, 0, stream, a);
+        else hipLaunchKernelGGL((decode_split_mfma<KV, QF, 4, true, kAppend>), dim3(grid), block, 0, stream, a);
+    }
+}
+
+// Kernels with the fused token write (lk_paged_decode_append) are separate instances, so the
+// plain decode does not reserve the write's registers.
 template <int KV, int QF>
 void launch_split_mfma(const DecodeArgs& a, uint32_t grid, hipStream_t stream) {
     const uint32_t waves = decode_waves(a, grid);
-    const dim3 block(kWave * waves);
-    if (a.shared_blocks) {
-        if (waves == 8) hipLaunchKernelGGL((decode_split_mfma<KV, QF, 8, false>), dim3(grid), block, 0, stream, a);
-        else hipLaunchKernelGGL((decode_split_mfma<KV, QF, 4, false>), dim3(grid), block, 0, stream, a);
-    } else {
-        if (waves == 8) hipLaunchKernelGGL((decode_split_mfma<KV, QF, 8, true>), dim3(grid), block, 0, stream, a);
-        else hipLaunchKernelGGL((decode_split_mfma<KV, QF, 4, true>), dim3(grid), block, 0, stream, a);
-    }
+    if (a.write_block != nullptr) launch_split_mfma_as<KV, QF, true>(a, waves, grid, stream);
+    else launch_split_mfma_as<KV, QF, false>(a, waves, grid, stream);
 }
+
+// Above this many splits the merge runs as four workgroups per (sequence, query head), one per
+// quarter of the dims (decode_combine_quarter). Measured on MI355X, FP8 records, per layer:
+// batch 1 @ 32,768 (32 splits) 18.9 -> 18.15 us, BF16 28.3 -> 27.55 us; batch 8 @ 4,096 (4
+// splits) 18.2 -> 18.35 us, so few splits keep one workgroup.
+constexpr uint32_t kQuarterSplits = 8;
 
 template <int QF>
 void launch_decode(const DecodeArgs& a, const Geometry& g, int kv, void* out, hipStream_t stream) {
@@ -239,7 +253,11 @@ void launch_decode(const DecodeArgs& a, const Geometry& g, int kv, void* out, hi
     if (a.out != nullptr) return;  // the split kernel wrote the output
     const dim3 grid(a.batch * a.query_heads);
     if (!vector_combine_fits(a)) hipLaunchKernelGGL((decode_combine<QF>), grid, dim3(kWave), 0, stream, a, out);
-    else if (a.splits <= kWave) hipLaunchKernelGGL((decode_combine_vector<QF, false>), grid, dim3(kWave), 0, stream, a, out);
+    else if (a.splits > kQuarterSplits) {
+        const dim3 quarters(a.batch * a.query_heads * 4);
+        if (a.splits <= kWave) hipLaunchKernelGGL((decode_combine_quarter<QF, false>), quarters, dim3(kWave), 0, stream, a, out);
+        else hipLaunchKernelGGL((decode_combine_quarter<QF, true>), quarters, dim3(kWave), 0, stream, a, out);
+    } else if (a.splits <= kWave) hipLaunchKernelGGL((decode_combine_vector<QF, false>), grid, dim3(kWave), 0, stream, a, out);
     else hipLaunchKernelGGL((decode_combine_vector<QF, true>), grid, dim3(kWave), 0, stream, a, out);
 }
 
