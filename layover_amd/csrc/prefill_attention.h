@@ -54,6 +54,17 @@ struct PrefillArgs {
     float* partial_ml;
 };
 
+// Maximum of three scores as one v_max3_f32. fmaxf chains compile to pairwise maxima with
+// each operand first canonicalized (IEEE mode), about three times the instructions; scores
+// are MFMA results or -inf, never signaling NaNs, so canonicalizing changes nothing. Not
+// volatile: the scheduler moves it like any VALU op. Measured on MI355X, 2,048-token chunk
+// at the end of a 32,768-token context: 1.00 -> 0.98 ms per layer.
+__device__ __forceinline__ float max3(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
 // The running maximum of a row that has seen no key yet: finite, so that a weight taken
 // against it is exp2(-inf) = 0 even when every score of the step is masked (a split can hold
 // no visible key for some of its rows), and its merge weight exp2(kNoMax - m) underflows to 0.
@@ -588,12 +599,12 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
     float raw_limit[2] = {-INFINITY, -INFINITY};  // BF16: (m + threshold) / scale per set
     auto lane_max = [&](const f32x4 (&s)[2], const Factors& f) __attribute__((always_inline)) {
         if constexpr (KV == LK_BF16) {
-            return fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])), fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
+            return max3(max3(s[0][0], s[0][1], s[0][2]), max3(s[0][3], s[1][0], s[1][1]), max3(s[1][2], s[1][3], s[1][3]));
         } else {
             float top_b[2];
 #pragma unroll
-            for (int b = 0; b < 2; ++b) top_b[b] = fmaxf(fmaxf(fmaxf(s[b][0], s[b][1]), s[b][2]), s[b][3]) * f.k[b];
-            return fmaxf(top_b[0], top_b[1]);
+            for (int b = 0; b < 2; ++b) top_b[b] = max3(max3(s[b][0], s[b][1], s[b][2]), s[b][3], s[b][3]) * f.k[b];
+            return max3(top_b[0], top_b[1], top_b[1]);
         }
     };
     auto exceeds = [&](int set, float lane_top) __attribute__((always_inline)) {
