@@ -189,17 +189,19 @@ __device__ __forceinline__ void decode_group_to(u32x4* __restrict__ target, int3
     const bool any_nan = __any((flags & 0x80808080u) != 0);
 
     if (!any_nan && shift >= -117 && shift <= 119) {
+        // Two codes to a BF16 pair in one scaled convert (v_cvt_scalef32_pk_bf16_fp8): the
+        // scale is an exact power of two and every product is a BF16 normal or zero, so the
+        // result is exact, as the float path it replaces (two converts to FP32, four
+        // multiplies, two permutes per four codes) was.
         const float scale = power_of_two(shift);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             u32x4 out;
 #pragma unroll
             for (int w = 0; w < 2; ++w) {
-                const int word = int(bytes[j][w]);
-                const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(word, false);
-                const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(word, true);
-                out[2 * w] = __builtin_amdgcn_perm(__float_as_uint(lo.y * scale), __float_as_uint(lo.x * scale), 0x07060302u);
-                out[2 * w + 1] = __builtin_amdgcn_perm(__float_as_uint(hi.y * scale), __float_as_uint(hi.x * scale), 0x07060302u);
+                const uint32_t word = bytes[j][w];
+                out[2 * w] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(word, scale, false));
+                out[2 * w + 1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(word, scale, true));
             }
             store_bf16<kNontemporal>(target + j * kWave + lane, out);
         }
