@@ -292,9 +292,10 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_mfma(PrefillArgs
 // ---------------------------------------------------------------------------------------
 // K/V shared through LDS. A workgroup of 4 waves owns 128 rows (32 per wave, as two sets of
 // 16) and walks the keys in steps of 32 (two blocks). Each step's K and V tiles (4 x 4 KiB)
-// are loaded once per workgroup: for BF16 pools by direct-to-LDS copies two steps ahead into
-// one of three buffers, for FP8 pools through registers one step ahead (the codes become BF16
-// on the way) into one of two. Per wave and step:
+// are loaded once per workgroup: for BF16 pools by direct-to-LDS copies into four buffers,
+// steps going in pairs (the next pair's copies issued when a pair starts, one barrier per
+// pair), for FP8 pools through registers one step ahead (the codes become BF16 on the way)
+// into one of two. Per wave and step:
 //   QK   for each block and set, four v_mfma_f32_16x16x32_bf16 on K read from LDS (lane
 //        (g, n): key n, dims 32g + 8j .. +8), reused by both sets;
 //   P    8 scores per lane (keys 4g..4g+3 of each block) of row n;
@@ -321,7 +322,9 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_mfma(PrefillArgs
 // causal compares and permlane-swapped row maxima, with V regrouped by 32 v_perm per step;
 // 1.18 ms with the transposing V reads, per-set stretches, masks only where needed and the
 // sums on the matrix cores; 1.13 ms with the lane-local rescale check; 1.10 ms with the
-// direct-to-LDS copies two steps ahead into the swizzled layout.
+// direct-to-LDS copies two steps ahead into the swizzled layout. Steps in pairs with one
+// barrier per pair (four buffers) against a barrier per step (three): 0.983-0.990 -> 0.970-0.977
+// ms there, and 0.057-0.058 -> 0.055-0.056 ms for a 2,048-token chunk at position 0.
 // O leaves through LDS: its rows are spread over lanes by dim (16e + n), so each wave writes
 // its 32 rows there and reads them back as 16-byte pieces of whole rows.
 constexpr uint32_t kLdsWaves = 4;
@@ -336,8 +339,8 @@ constexpr uint32_t kLdsRowBytes = kDim * 2 + 16;         // 272: rows of the out
 constexpr uint32_t kRegionStride = 1024 + 16;
 constexpr uint32_t kLdsTile = 4 * kRegionStride;         // one block's K or V
 constexpr uint32_t kLdsStep = 4 * kLdsTile;              // K0, K1, V0, V1
-constexpr uint32_t kLdsAllocated = 3;  // step buffers allocated (FP8 rotates through two)
-static_assert(kLdsWaves * kLdsRows * kLdsRowBytes <= kLdsAllocated * kLdsStep, "the output staging must fit the step buffers");
+constexpr uint32_t kLdsAllocated = 4;  // step buffers allocated (FP8 rotates through two)
+static_assert(kLdsWaves * kLdsRows * kLdsRowBytes <= 3 * kLdsStep, "the output staging must fit three step buffers");
 
 // Byte offset of key `key`'s 16-byte chunk `chunk` (dims 8 chunk .. +8) inside a K or V tile.
 __device__ __forceinline__ uint32_t k_slot(uint32_t key, uint32_t chunk) {
@@ -347,11 +350,11 @@ __device__ __forceinline__ uint32_t v_slot(uint32_t key, uint32_t chunk) {
     return (chunk / 4) * kRegionStride + key * 64 + 16 * (chunk % 4);
 }
 
-// BF16 pools copy each step straight into LDS two steps ahead (three buffers); FP8 pools
-// convert their codes on the way, through registers, one step ahead (two buffers).
+// BF16 pools copy each pair of steps straight into LDS one pair ahead (four buffers); FP8
+// pools convert their codes on the way, through registers, one step ahead (two buffers).
 template <int KV>
 constexpr uint32_t lds_buffers() {
-    return KV == LK_BF16 ? 3 : 2;
+    return KV == LK_BF16 ? 4 : 2;
 }
 constexpr uint32_t kCopiesPerStep = 4;  // 16-byte-per-lane copies per wave and step (BF16)
 
@@ -374,7 +377,7 @@ template <int KV>
 __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_eu(2, 2))) void prefill_mfma_lds(PrefillArgs a) {
     constexpr uint32_t kLdsBuffers = lds_buffers<KV>();
     static_assert(kLdsBuffers <= kLdsAllocated, "more step buffers than allocated");
-    __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsAllocated][kLdsStep];
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBuffers > 3 ? kLdsBuffers : 3][kLdsStep];
     __shared__ int32_t lds_shift[kLdsBuffers][4];  // FP8: per buffer, the shift of K0, K1, V0, V1
     const uint32_t lane = threadIdx.x % kWave;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -476,9 +479,9 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
     // chunk the layout puts there: for K key 4x + t/16, chunk (t % 16) ^ 4(t/16); for V key
     // t/4, chunk 4x + t % 4. The copies are issued as inline assembly, which the compiler's wait
     // counting does not see (it would otherwise wait for them before any LDS read it cannot
-    // prove disjoint); they are waited for only at the barrier before their step is read (see
-    // step_barrier), which relies on exactly kCopiesPerStep of them per wave and step and no
-    // other vector-memory loads in the loop (block ids are scalar loads).
+    // prove disjoint); they are waited for only at the barrier before their step is read (the
+    // pair's step_barrier, which waits for all of this wave's vector-memory operations; block ids are
+    // scalar loads).
     const auto* scalar_ids = (const __attribute__((address_space(4))) int32_t*)a.block_ids;
     const uint32_t wave_part = __builtin_amdgcn_readfirstlane(part);
     const uint32_t copy_src = wave_part < 2 ? (piece / 16) * 256 + 16 * ((piece % 16) ^ (4 * (piece / 16))) : (piece / 4) * 256 + 16 * (piece % 4);
@@ -495,13 +498,10 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
                          "s"(__builtin_amdgcn_readfirstlane(dst + kRegionStride * x))
                          : "memory", "m0");
     };
-    // The end of a BF16 step: this wave's copies of the step after next may stay in flight; the
-    // older ones, which fill the next step's buffer, must have landed, and every LDS read of
-    // this step must be done before any wave refills its buffer.
-    auto step_barrier = [&](bool copies_in_flight) __attribute__((always_inline)) {
-        static_assert(kCopiesPerStep == 4, "the wait below counts the copies");
-        if (copies_in_flight) asm volatile("s_waitcnt vmcnt(4) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // The end of a BF16 pair of steps: this wave's copies of the next pair must have landed,
+    // and every LDS read of this pair must be done before any wave refills its buffers.
+    auto step_barrier = [&]() __attribute__((always_inline)) {
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
     };
 
     // Running maximum per row (lane (g, n): row n of each set); output and, for BF16 pools,
@@ -671,7 +671,12 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
     auto run_step = [&](uint32_t step, auto masked_tag) __attribute__((always_inline)) {
         constexpr bool kMasked = decltype(masked_tag)::value;
         if constexpr (KV == LK_BF16) {
-            if (step + 2 < steps) copy_step_tiles(step + 2);
+            // Steps go in pairs (first_step + 2i, + 2i + 1): the next pair's copies go out
+            // when a pair starts, and only the pair's last step ends at the barrier.
+            if ((step - first_step) % 2 == 0) {
+                if (step + 2 < steps) copy_step_tiles(step + 2);
+                if (step + 3 < steps) copy_step_tiles(step + 3);
+            }
         }
         const Factors f = factors(step);
         bf16x8 kk[2][4];
@@ -718,7 +723,7 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
         __builtin_amdgcn_s_setprio(0);
         accumulate(1, p1, vb);
         if constexpr (KV == LK_BF16) {
-            step_barrier(step + 2 < steps);
+            if ((step - first_step) % 2 == 1 || step + 1 == steps) step_barrier();
         } else {
             if (step + 1 < steps) {
                 store_step((step + 1) % kLdsBuffers, staged);
@@ -735,7 +740,7 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
             __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
             copy_step_tiles(first_step);
             if (first_step + 1 < steps) copy_step_tiles(first_step + 1);
-            step_barrier(false);
+            step_barrier();  // the first pair's tiles are in
         } else {
             load_step(first_step, staged);
             store_step(first_step % kLdsBuffers, staged);
