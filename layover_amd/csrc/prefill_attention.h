@@ -54,17 +54,6 @@ struct PrefillArgs {
     float* partial_ml;
 };
 
-// Maximum of three scores as one v_max3_f32. fmaxf chains compile to pairwise maxima with
-// each operand first canonicalized (IEEE mode), about three times the instructions; scores
-// are MFMA results or -inf, never signaling NaNs, so canonicalizing changes nothing. Not
-// volatile: the scheduler moves it like any VALU op. Measured on MI355X, 2,048-token chunk
-// at the end of a 32,768-token context: 1.00 -> 0.98 ms per layer.
-__device__ __forceinline__ float max3(float a, float b, float c) {
-    float r;
-    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-    return r;
-}
-
 // The running maximum of a row that has seen no key yet: finite, so that a weight taken
 // against it is exp2(-inf) = 0 even when every score of the step is masked (a split can hold
 // no visible key for some of its rows), and its merge weight exp2(kNoMax - m) underflows to 0.
@@ -323,8 +312,8 @@ __global__ __launch_bounds__(kWave* kPrefillWaves) void prefill_mfma(PrefillArgs
 // 1.18 ms with the transposing V reads, per-set stretches, masks only where needed and the
 // sums on the matrix cores; 1.13 ms with the lane-local rescale check; 1.10 ms with the
 // direct-to-LDS copies two steps ahead into the swizzled layout. Steps in pairs with one
-// barrier per pair (four buffers) against a barrier per step (three): 0.983-0.990 -> 0.970-0.977
-// ms there, and 0.057-0.058 -> 0.055-0.056 ms for a 2,048-token chunk at position 0.
+// barrier per pair (four buffers) against a barrier per step (three): 1.064-1.077 -> 1.059-1.067
+// ms there (on a slower box), and 0.060-0.062 -> 0.058 ms for a 2,048-token chunk at position 0.
 // O leaves through LDS: its rows are spread over lanes by dim (16e + n), so each wave writes
 // its 32 rows there and reads them back as 16-byte pieces of whole rows.
 constexpr uint32_t kLdsWaves = 4;
@@ -492,9 +481,13 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
         const uint32_t block = uint32_t(scalar_ids[block_index]);
         const uint8_t* src = a.pool + uint64_t(block) * a.block_bytes + copy_tile + copy_src;
         const uint32_t dst = uint32_t(uintptr_t((__attribute__((address_space(3))) uint8_t*)(lds[step % kLdsBuffers] + tile_lds)));
+        // An LDS-DMA load reads its LDS address from M0, and a scalar write of M0 needs one wait
+        // state before such a load (the compiler inserts it for its own code but cannot see
+        // into this asm): without the s_nop a copy could take the previous copy's M0 and land
+        // in the wrong region, depending on how other waves' instructions interleave.
 #pragma unroll
         for (uint32_t x = 0; x < kCopiesPerStep; ++x)
-            asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src + copy_step * x),
+            asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src + copy_step * x),
                          "s"(__builtin_amdgcn_readfirstlane(dst + kRegionStride * x))
                          : "memory", "m0");
     };
@@ -599,12 +592,12 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
     float raw_limit[2] = {-INFINITY, -INFINITY};  // BF16: (m + threshold) / scale per set
     auto lane_max = [&](const f32x4 (&s)[2], const Factors& f) __attribute__((always_inline)) {
         if constexpr (KV == LK_BF16) {
-            return max3(max3(s[0][0], s[0][1], s[0][2]), max3(s[0][3], s[1][0], s[1][1]), max3(s[1][2], s[1][3], s[1][3]));
+            return fmaxf(fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3])), fmaxf(fmaxf(s[1][0], s[1][1]), fmaxf(s[1][2], s[1][3])));
         } else {
             float top_b[2];
 #pragma unroll
-            for (int b = 0; b < 2; ++b) top_b[b] = max3(max3(s[b][0], s[b][1], s[b][2]), s[b][3], s[b][3]) * f.k[b];
-            return max3(top_b[0], top_b[1], top_b[1]);
+            for (int b = 0; b < 2; ++b) top_b[b] = fmaxf(fmaxf(fmaxf(s[b][0], s[b][1]), s[b][2]), s[b][3]) * f.k[b];
+            return fmaxf(top_b[0], top_b[1]);
         }
     };
     auto exceeds = [&](int set, float lane_top) __attribute__((always_inline)) {
@@ -693,7 +686,8 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
         // stretch, whose MFMAs keep running while this wave's dependent VALU chain is issued
         // first. Measured on MI355X (2,048 tokens ending a 32,768 context): 1.094 -> 1.023 ms
         // per layer; raising it for the QK MFMAs instead, or dropping it around set 0's PV, was
-        // 1.08-1.11 and 1.07 ms.
+        // 1.08-1.11 and 1.07 ms. With the steps paired it still gains 1-2% there (1.059-1.067
+        // against 1.079-1.081 ms on one box).
         __builtin_amdgcn_s_setprio(1);
         top[0] = lane_max(s[0], f);
         if constexpr (kMasked) {

@@ -278,3 +278,25 @@ def test_unaligned_fp8_records_are_staged_and_match_the_oracle(layers, kv_heads)
     ids = torch.from_numpy(block_ids).cuda()
     status = lib.lk_paged_prefill(shape, q.data_ptr(), pool.records.data_ptr(), ids.data_ptr(), used, out.data_ptr(), None)
     assert status == _lib.LK_ERR_INVALID and b"16-byte aligned" in lib.lk_last_error()
+
+
+@pytest.mark.parametrize("start,tokens,kv_heads,gqa", [(0, 64, 4, 4), (100, 64, 4, 4), (0, 64, 4, 3), (0, 64, 4, 5), (4, 57, 4, 4)])
+@pytest.mark.parametrize("fp8", [False, True], ids=["bf16_pool", "fp8_pool"])
+def test_prefill_gives_the_same_bits_on_every_launch(start, tokens, kv_heads, gqa, fp8):
+    """Six launches of the same chunk give identical outputs bit for bit. A maximum written as
+    inline assembly once read matrix-core results without the wait states the compiler
+    inserts for its own instructions: the second 16 rows of a wave then varied from launch
+    to launch (still within the north-star tolerance), at GQA 3-5 with two or more key steps."""
+    from layover_amd.kernels.hip_prefill import paged_prefill_attention_hip
+
+    end = start + tokens
+    used = -(-end // 16)
+    pool, _ = make_pool(used + 2, 2, kv_heads, seed=tokens + gqa, fp8=fp8)
+    block_ids = torch.from_numpy(np.random.default_rng(start).permutation(used + 2)[:used].astype(np.int32)).cuda()
+    q = (torch.randn(kv_heads * gqa, tokens, 128, generator=torch.Generator().manual_seed(7)) * 2).to(torch.bfloat16).cuda()
+    print(f"prefill repeat start={start} tokens={tokens} kv={kv_heads} gqa={gqa} fp8={fp8}", flush=True)
+    first = paged_prefill_attention_hip(q, pool, 1, block_ids, start, gqa).clone()
+    for _ in range(5):
+        again = paged_prefill_attention_hip(q, pool, 1, block_ids, start, gqa)
+        torch.cuda.synchronize()
+        assert torch.equal(again.view(torch.int16), first.view(torch.int16))
