@@ -142,8 +142,11 @@ int lk_paged_prefill(const lk_prefill_shape* shape, const void* q, const void* p
 
 /* Bytes of device workspace lk_paged_prefill_split needs for this shape: for an FP8-record pool,
  * the chunk's history decoded to BF16 (one layer: 4 KiB per token at 8 KV heads) plus a block
- * index; and split-K partials when the chunk's (KV head, 128-row tile) workgroups would not
- * give every CU two of them (short chunks against long histories). 0 when neither applies.
+ * index; split-K partials when the chunk's (KV head, 128-row tile) workgroups would not give
+ * every CU two of them (short chunks against long histories); and, when they give exactly
+ * that and causal tiles differ widely (chunks near the start of a sequence), the states of
+ * heavy tiles whose key steps two workgroups of a CU divide (80 KiB per side) with a tag and a
+ * ready word per CU pair. 0 when none applies.
  * No counterpart in the reference, whose prefill gathers the history and runs FlashAttention;
  * depends on the shape and the device's CU count (LAYOVER_PREFILL_SPLITS=n forces n splits;
  * LAYOVER_PREFILL_FP8=direct reads FP8 records in the attention kernel instead of staging
@@ -151,9 +154,10 @@ int lk_paged_prefill(const lk_prefill_shape* shape, const void* q, const void* p
 uint64_t lk_paged_prefill_workspace(const lk_prefill_shape* shape);
 
 /* lk_paged_prefill, staging an FP8-record history as BF16 first and splitting each tile's keys
- * over several workgroups when the plan above does (partials merged in a further launch). The
- * workspace (at least lk_paged_prefill_workspace bytes, 16-byte aligned; may be null when that
- * is 0) needs no initialization; calls that share one must not overlap in time. */
+ * over several workgroups when the plan above does (partials merged in a further launch), or
+ * dividing heavy tiles within CU pairs (merged in the same launch). The workspace (at least
+ * lk_paged_prefill_workspace bytes, 16-byte aligned; may be null when that is 0) needs no
+ * initialization; calls that share one must not overlap in time. */
 int lk_paged_prefill_split(const lk_prefill_shape* shape, const void* q, const void* pool, const int32_t* block_ids,
                            uint32_t num_block_ids, void* out, void* workspace, uint64_t workspace_bytes, void* stream);
 

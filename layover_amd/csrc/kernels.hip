@@ -6,6 +6,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
+#include <chrono>
 #include <mutex>
 #include <stdexcept>
 #include <string>
@@ -741,7 +743,33 @@ struct PrefillPlan {
     uint32_t split_steps;
     bool shared;      // the LDS kernel (the register-only one never splits)
     bool stage_fp8;   // FP8 pool decoded into the workspace first
+    bool paired;      // the grid is resident at once, two workgroups per CU
+    bool pair_halves; // paired, unsplit, and some CU pair's heavy tile divides its steps
+    int32_t pair_bias;
 };
+
+// Steps moved toward the heavy side of a divided tile (the partner side pays a second
+// prologue and epilogue); LAYOVER_PREFILL_PAIR_BIAS overrides it, read per launch.
+constexpr int32_t kPairBias = 12;
+
+// Key steps of a 128-row tile of the LDS kernel, and whether a CU pair divides its heavy
+// tile: the same arithmetic as prefill_mfma_lds's job plan.
+uint32_t lds_tile_steps(uint64_t start, uint64_t rows, uint32_t groups, uint64_t tile) {
+    const uint64_t tile_rows = uint64_t(kLdsRows) * kLdsWaves;
+    const uint64_t last_row = ((tile + 1) * tile_rows < rows ? (tile + 1) * tile_rows : rows) - 1;
+    return uint32_t(((start + last_row / groups) / kSlots + 2) / 2);
+}
+bool any_pair_divides(const lk_prefill_shape& s, uint64_t row_tiles, int32_t bias) {
+    const uint32_t groups = s.query_heads / s.kv_heads;
+    const uint64_t rows = uint64_t(s.tokens) * groups, half = (row_tiles + 1) / 2;
+    for (uint64_t light = 0; light + half < row_tiles; ++light) {
+        const uint32_t heavy_steps = lds_tile_steps(s.start, rows, groups, row_tiles - 1 - light);
+        const int64_t share = (int64_t(heavy_steps) + lds_tile_steps(s.start, rows, groups, light) + bias + 1) / 2;
+        const uint32_t cut = uint32_t(share < 1 ? 1 : share);
+        if (cut < heavy_steps && uint64_t(heavy_steps - cut) * 8 >= heavy_steps) return true;
+    }
+    return false;
+}
 
 // CUs of the current device, cached per device; 256 (MI355X) when no device answers, with the
 // failed query's error cleared so that it is not reported by a later check.
@@ -796,20 +824,43 @@ PrefillPlan prefill_plan(const lk_prefill_shape& s) {
     }
     const uint32_t most = kMaxKeySplits < max_steps ? kMaxKeySplits : max_steps;
     wanted = wanted < 1 ? 1 : (wanted > most ? most : wanted);
-    if (wanted <= 1) return p;
-    p.split_steps = (max_steps + wanted - 1) / wanted;
-    p.key_splits = (max_steps + p.split_steps - 1) / p.split_steps;
+    if (wanted > 1) {
+        p.split_steps = (max_steps + wanted - 1) / wanted;
+        p.key_splits = (max_steps + p.split_steps - 1) / p.split_steps;
+    }
+    p.paired = p.row_tiles * s.kv_heads * p.key_splits <= 2ull * compute_units();
+    // Paired, unsplit chunks divide their heavy tiles' keys within each CU pair where that pays
+    // (LAYOVER_PREFILL_PAIR_HALVES=0 turns it off, read per launch).
+    const char* halves = getenv("LAYOVER_PREFILL_PAIR_HALVES");
+    const char* bias = getenv("LAYOVER_PREFILL_PAIR_BIAS");
+    p.pair_bias = bias ? int32_t(strtol(bias, nullptr, 10)) : kPairBias;
+    p.pair_halves = p.paired && p.key_splits == 1 && !(halves && strcmp(halves, "0") == 0) && any_pair_divides(s, p.row_tiles, p.pair_bias);
     return p;
 }
 
-// Workspace layout: [staged BF16 history | staged block index | split partials], each part
-// 256-byte aligned; parts the plan does not use are absent.
+// Workspace layout: [staged BF16 history | staged block index | split partials | pair states |
+// pair tags and ready words], each part 256-byte aligned; parts the plan does not use are absent.
 struct PrefillWorkspace {
-    uint64_t stage_bytes, index_bytes, partial_bytes;
-    uint64_t total() const { return stage_bytes + index_bytes + partial_bytes; }
+    uint64_t stage_bytes, index_bytes, partial_bytes, pair_state_bytes, pair_tag_bytes;
+    uint64_t total() const { return stage_bytes + index_bytes + partial_bytes + pair_state_bytes + pair_tag_bytes; }
 };
 
 uint64_t round_up_256(uint64_t bytes) { return (bytes + 255) / 256 * 256; }
+
+// Pair tags: even, distinct for every launch of the process, and with a start drawn from the
+// clock and an address, so that tags left in a reused workspace by another process do not
+// repeat either. A side swaps tag | side into its tile's word.
+uint64_t next_pair_tag() {
+    static const int anchor = 0;
+    static std::atomic<uint64_t> counter{[] {
+        uint64_t x = uint64_t(std::chrono::steady_clock::now().time_since_epoch().count()) ^ uint64_t(uintptr_t(&anchor));
+        x += 0x9E3779B97F4A7C15ull;  // splitmix64 finalizer
+        x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+        x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+        return x ^ (x >> 31);
+    }()};
+    return counter.fetch_add(1, std::memory_order_relaxed) << 1;
+}
 
 uint64_t staged_block_bytes(const lk_prefill_shape& s) { return uint64_t(2) * s.kv_heads * kSlots * kDim * 2; }
 
@@ -823,6 +874,11 @@ PrefillWorkspace prefill_workspace_parts(const lk_prefill_shape& s, const Prefil
     if (p.key_splits > 1) {
         const uint64_t rows = uint64_t(s.tokens) * (s.query_heads / s.kv_heads);
         w.partial_bytes = uint64_t(s.kv_heads) * rows * p.key_splits * (kDim + 2) * sizeof(float);
+    }
+    if (p.pair_halves) {
+        const uint64_t tiles = uint64_t(s.kv_heads) * ((p.row_tiles + 1) / 2);  // CU pairs
+        w.pair_state_bytes = round_up_256(tiles * 2 * kPairStateFloats * kWave * kLdsWaves * sizeof(float));
+        w.pair_tag_bytes = round_up_256(tiles * 2 * sizeof(uint64_t));  // tags, then ready words
     }
     return w;
 }
@@ -857,6 +913,8 @@ void run_prefill(const lk_prefill_shape& s, const void* q, const void* pool, con
         p.key_splits = 1;
         p.split_steps = uint32_t((((end + kSlots - 1) / kSlots) + 1) / 2);
         p.stage_fp8 = false;
+        p.paired = p.row_tiles * s.kv_heads <= 2ull * compute_units();
+        p.pair_halves = false;
     }
     // Staged records are read 2 bytes at a time and need only be even; everything read in
     // place, and q and out, must be 16-byte aligned.
@@ -888,10 +946,19 @@ void run_prefill(const lk_prefill_shape& s, const void* q, const void* pool, con
     a.scale_log2 = s.scale * kLog2e;
     a.key_splits = p.key_splits;
     a.split_steps = p.split_steps;
-    a.paired = grid <= 2ull * compute_units() ? 1u : 0u;
+    a.paired = p.paired ? 1u : 0u;
     uint8_t* const space = static_cast<uint8_t*>(workspace);
     a.partial_acc = p.key_splits > 1 ? reinterpret_cast<float*>(space + parts.stage_bytes + parts.index_bytes) : nullptr;
     a.partial_ml = p.key_splits > 1 ? a.partial_acc + uint64_t(s.kv_heads) * rows * p.key_splits * kDim : nullptr;
+    if (p.pair_halves) {
+        uint8_t* const pair_space = space + parts.stage_bytes + parts.index_bytes + parts.partial_bytes;
+        a.pair_halves = 1;
+        a.pair_state = reinterpret_cast<uint32_t*>(pair_space);
+        a.pair_tags = reinterpret_cast<uint64_t*>(pair_space + parts.pair_state_bytes);
+        a.pair_ready = a.pair_tags + uint64_t(s.kv_heads) * ((p.row_tiles + 1) / 2);
+        a.pair_tag = next_pair_tag();
+        a.pair_bias = p.pair_bias;
+    }
     if (p.stage_fp8) {
         // The history's blocks, this layer only, as a one-layer BF16 pool; the BF16 kernel then
         // reads block b of it through index[b] = b.

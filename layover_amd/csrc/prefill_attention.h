@@ -52,7 +52,32 @@ struct PrefillArgs {
     uint32_t paired;
     float* partial_acc;
     float* partial_ml;
+    // Paired key halves (paired grids without key splits, given a workspace). A CU pair is a
+    // heavy tile's workgroup (order < half) and its partner (order + half), which takes the
+    // light tile. When the heavy tile has more steps than half the pair's work, the heavy
+    // workgroup stops at about that half and the partner, after its light tile, takes the heavy
+    // tile's remaining steps. Each side writes its unnormalized state to
+    // pair_state[(kv head, pair, side)] and swaps pair_tag | side into
+    // pair_tags[(kv head, pair)] (pair: the light tile's index); the side that finds its
+    // partner's tag of this launch there merges both, in side order, and writes out. Only the
+    // first side stores its state, then publishes its tag in pair_ready[(kv head, pair)].
+    // pair_tag is unique per launch, so neither word needs clearing. pair_bias (steps) moves the split
+    // point toward the heavy side, for the partner's second prologue and epilogue.
+    uint32_t pair_halves;
+    int32_t pair_bias;
+    uint64_t pair_tag;
+    uint32_t* pair_state;
+    uint64_t* pair_tags;
+    uint64_t* pair_ready;
 };
+
+// Polls of a partner's ready word (each after a short sleep) before the merging side gives up
+// and writes NaN: about a second, far beyond the microseconds a resident partner needs.
+constexpr uint32_t kPairWaitBound = 1u << 22;
+
+// Floats of one workgroup's state in the pair merge: per thread, 64 accumulators of its rows
+// and dims, then the 8 rows' maxima and 8 weight totals, in 16-byte pieces, thread-fastest.
+constexpr uint32_t kPairStateFloats = 80;
 
 // The running maximum of a row that has seen no key yet: finite, so that a weight taken
 // against it is exp2(-inf) = 0 even when every score of the step is masked (a split can hold
@@ -368,6 +393,8 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
     static_assert(kLdsBuffers <= kLdsAllocated, "more step buffers than allocated");
     __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBuffers > 3 ? kLdsBuffers : 3][kLdsStep];
     __shared__ int32_t lds_shift[kLdsBuffers][4];  // FP8: per buffer, the shift of K0, K1, V0, V1
+    __shared__ uint32_t pair_merges;               // this workgroup merges its pair's states
+    __shared__ uint32_t pair_lost;                 // ... but its partner's state never came
     const uint32_t lane = threadIdx.x % kWave;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const uint32_t g = lane / 16;
@@ -380,20 +407,59 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
     const uint32_t split = (blockIdx.x / a.kv_heads) % a.key_splits;
     const uint32_t order = blockIdx.x / (a.kv_heads * a.key_splits);
     const uint32_t half = (a.row_tiles + 1) / 2;
-    const uint32_t tile = a.paired && order >= half ? order - half : a.row_tiles - 1 - order;
     const uint32_t total_rows = a.tokens * a.groups;
+    const uint32_t end = a.start + a.tokens;
+    const uint32_t last_block = (end + kSlots - 1) / kSlots - 1;
+    // Key steps of a tile: up to its last row's limit, in steps of two blocks.
+    auto steps_of = [&](uint32_t t) __attribute__((always_inline)) {
+        const uint32_t last_row = min((t + 1) * kLdsWaves * kLdsRows, total_rows) - 1;
+        const uint32_t key_blocks = (a.start + last_row / a.groups) / kSlots + 1;
+        return (key_blocks + 1) / 2;
+    };
+
+    // Jobs: (tile, steps [first, last), pair part 0 none / 1 heavy side / 2 partner side).
+    uint32_t jobs = 1;
+    uint32_t job_tile[2], job_first[2], job_last[2], job_part[2];
+    {
+        const uint32_t tile = a.paired && order >= half ? order - half : a.row_tiles - 1 - order;
+        const uint32_t tile_steps = steps_of(tile);
+        job_tile[0] = tile;
+        job_first[0] = min(split * a.split_steps, tile_steps);
+        job_last[0] = min(job_first[0] + a.split_steps, tile_steps);
+        job_part[0] = 0;
+        if (a.pair_halves) {
+            // The heavy tile of this CU pair and where its steps divide: about equal work on
+            // both sides; no division when the light tile already carries as much.
+            const uint32_t light = order < half ? order : order - half;
+            const bool partnered = light + half < a.row_tiles;
+            const uint32_t heavy = a.row_tiles - 1 - light;
+            const uint32_t heavy_steps = steps_of(heavy);
+            const int64_t share = (int64_t(heavy_steps) + steps_of(light) + a.pair_bias + 1) / 2;
+            const uint32_t cut = uint32_t(share < 1 ? 1 : share);
+            // Only when the moved steps are worth a merge: at least an eighth of the tile (long
+            // histories, where paired tiles differ by a few percent, stay whole).
+            if (partnered && cut < heavy_steps && (heavy_steps - cut) * 8 >= heavy_steps) {
+                if (order < half) {
+                    job_last[0] = cut;
+                    job_part[0] = 1;
+                } else {
+                    jobs = 2;
+                    job_tile[1] = heavy;
+                    job_first[1] = cut;
+                    job_last[1] = heavy_steps;
+                    job_part[1] = 2;
+                }
+            }
+        }
+    }
+
+    for (uint32_t job = 0; job < jobs; ++job) {
+    const uint32_t tile = job_tile[job];
     const uint32_t wg_row0 = tile * kLdsWaves * kLdsRows;
     const uint32_t row0 = wg_row0 + wave * kLdsRows;
-    const uint32_t end = a.start + a.tokens;
-
-    // Keys the workgroup needs: up to its last row's limit; in steps of two blocks.
-    const uint32_t wg_last = min(wg_row0 + kLdsWaves * kLdsRows, total_rows) - 1;
-    const uint32_t key_blocks = (a.start + wg_last / a.groups) / kSlots + 1;
-    const uint32_t tile_steps = (key_blocks + 1) / 2;
-    // This workgroup's steps [first_step, steps); a split past the tile's keys does none.
-    const uint32_t first_step = min(split * a.split_steps, tile_steps);
-    const uint32_t steps = min(first_step + a.split_steps, tile_steps);
-    const uint32_t last_block = (end + kSlots - 1) / kSlots - 1;
+    // This job's steps [first_step, steps); a split past the tile's keys does none.
+    const uint32_t first_step = job_first[job];
+    const uint32_t steps = job_last[job];
     // The wave's first row's limit (later rows only see more keys); -1 for a wave past the end.
     const int64_t first_limit = row0 < total_rows ? int64_t(a.start) + row0 / a.groups : -1;
 
@@ -781,21 +847,109 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
 
     // Row totals in the layout of O: lane (g, n) needs rows 4g + r. FP8 pools summed per lane
     // (row n, a quarter of the keys each): reduce over the lane groups, then fetch row 4g + r.
-    float inverse[2][4];
+    float row_total[2][4];
 #pragma unroll
     for (int set = 0; set < 2; ++set) {
         if constexpr (KV == LK_BF16) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) inverse[set][r] = 1.0f / sums[set][r];
+            for (int r = 0; r < 4; ++r) row_total[set][r] = sums[set][r];
         } else {
             float total = l[set];
             total += __shfl_xor(total, 16, kWave);
             total += __shfl_xor(total, 32, kWave);
-            const float own = 1.0f / total;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) inverse[set][r] = __shfl(own, int(4 * g + r), kWave);
+            for (int r = 0; r < 4; ++r) row_total[set][r] = __shfl(total, int(4 * g + r), kWave);
         }
     }
+
+    if (job_part[job] != 0) {
+        // One side of a divided heavy tile. Both sides have the same rows in the same lanes, so
+        // thread t's state meets thread t's. A side announces itself by swapping its tag into
+        // the pair's word. The first to arrive stores its state with agent-scope stores (past
+        // the XCD's own L2, which other XCDs do not see), waits for every store, and then
+        // publishes its tag in the pair's ready word. The second finds the first's tag in the
+        // pair's word; the first is then resident and has nothing left to wait for, so the
+        // second waits for the ready word (with a bound that turns a lost partner into NaN
+        // output, not a hang), reads the state with agent-scope loads and merges. The merge
+        // takes side 1's state first whichever side runs it, so the output bits do not depend
+        // on which side arrived last.
+        const uint32_t self = job_part[job] - 1;
+        const uint64_t pair_index = uint64_t(kv_head) * half + (a.row_tiles - 1 - tile);  // the pair's light tile
+        constexpr uint32_t kSideBytes = kPairStateFloats * 4 * kWave * kLdsWaves;
+        const auto side = [&](uint32_t which) __attribute__((always_inline)) {
+            return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<uint8_t*>(a.pair_state) + (pair_index * 2 + which) * kSideBytes, short(0),
+                                                     int(kSideBytes), 0x00020000);
+        };
+        const __amdgpu_buffer_rsrc_t own = side(self), other = side(1 - self);
+        // Thread t's 16-byte piece c sits at (256 c + t) x 16: pieces 0-15 the accumulators
+        // o[set][e] (rows 4g + r), 16-17 the rows' maxima, 18-19 their weight totals.
+        constexpr int kAgent = 16;  // cache policy: coherent at agent scope (past the XCD's L2)
+        const auto at = [&](uint32_t piece) __attribute__((always_inline)) { return (piece * kWave * kLdsWaves + threadIdx.x) * 16; };
+        f32x4 row_m[2], totals[2];
+#pragma unroll
+        for (int set = 0; set < 2; ++set)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                row_m[set][r] = __shfl(m[set], int(4 * g + r), kWave);
+                totals[set][r] = row_total[set][r];
+            }
+        if (threadIdx.x == 0) {
+            const uint64_t found = __hip_atomic_exchange(a.pair_tags + pair_index, a.pair_tag | self, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            pair_merges = found == (a.pair_tag | (1 - self)) ? 1u : 0u;
+        }
+        __syncthreads();
+        if (!pair_merges) {
+#pragma unroll
+            for (int set = 0; set < 2; ++set) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[set][e]), own, at(set * 8 + e), 0, kAgent);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, row_m[set]), own, at(16 + set), 0, kAgent);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, totals[set]), own, at(18 + set), 0, kAgent);
+            }
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (threadIdx.x == 0) __hip_atomic_store(a.pair_ready + pair_index, a.pair_tag | self, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            continue;  // the partner merges (a later job, if any, starts clean)
+        }
+        if (threadIdx.x == 0) {
+            uint32_t tries = 0;
+            while (__hip_atomic_load(a.pair_ready + pair_index, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != (a.pair_tag | (1 - self)) &&
+                   ++tries < kPairWaitBound)
+                __builtin_amdgcn_s_sleep(2);
+            pair_lost = tries < kPairWaitBound ? 0u : 1u;
+        }
+        __syncthreads();
+        const bool lost = pair_lost != 0;
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int set = 0; set < 2; ++set) {
+            const f32x4 m_in = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(other, at(16 + set), 0, kAgent));
+            const f32x4 total_in = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(other, at(18 + set), 0, kAgent));
+            f32x4 o_in[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o_in[e] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(other, at(set * 8 + e), 0, kAgent));
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float m0 = self == 0 ? row_m[set][r] : m_in[r], m1 = self == 0 ? m_in[r] : row_m[set][r];
+                const float t0 = self == 0 ? totals[set][r] : total_in[r], t1 = self == 0 ? total_in[r] : totals[set][r];
+                const float top = fmaxf(m0, m1);
+                const float w0 = exp2_fast(m0 - top), w1 = exp2_fast(m1 - top);  // kNoMax sides: 0
+                row_total[set][r] = fmaf(t0, w0, t1 * w1);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float o0 = self == 0 ? o[set][e][r] : o_in[e][r], o1 = self == 0 ? o_in[e][r] : o[set][e][r];
+                    o[set][e][r] = fmaf(o0, w0, o1 * w1);
+                }
+                if (lost) row_total[set][r] = __builtin_nanf("");
+            }
+        }
+    }
+
+    float inverse[2][4];
+#pragma unroll
+    for (int set = 0; set < 2; ++set)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) inverse[set][r] = 1.0f / row_total[set][r];
 
     // O through LDS (the loop's last barrier has released the buffers): row 16 set + 4g + r,
     // dim 16e + n of this wave's 32 rows, then whole rows out in 16-byte pieces.
@@ -820,6 +974,8 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
             *reinterpret_cast<u32x4*>(a.out + (uint64_t(out_head) * a.tokens + out_token) * kDim + 8 * (piece_index % 16)) =
                 *reinterpret_cast<const u32x4*>(staging + local_row * kLdsRowBytes + 16 * (piece_index % 16));
         }
+    }
+    if (job + 1 < jobs) __syncthreads();  // the staging rows are the next job's step buffers
     }
 }
 

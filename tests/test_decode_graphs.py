@@ -195,6 +195,28 @@ def test_prefill_split_plan_sizes_its_workspace(monkeypatch):
     assert lib.lk_paged_prefill_workspace(bad) == 0
 
 
+def test_prefill_pair_halves_size_their_workspace(monkeypatch):
+    """A 2,048-token chunk at position 0 (512 resident workgroups, causal tiles of 1 to 64 key
+    steps) divides its heavy tiles within CU pairs: per (KV head, pair) two sides' states of
+    256 threads x 80 floats, then a tag and a ready word, each part 256-byte aligned. A chunk
+    ending a 32,768 context divides nothing (its paired tiles differ by a few percent) and
+    needs no workspace; LAYOVER_PREFILL_PAIR_HALVES=0 turns the division off, and a bias that
+    leaves the heavy tiles whole does too."""
+    from layover_amd.kernels import _lib
+
+    lib = _lib.load()
+    at_zero = _lib.PrefillShape(2048, 0, 32, 8, 128, 36, 16, 0, _lib.LK_BF16, _lib.LK_BF16, 128**-0.5)
+    pairs = 8 * 32
+    assert lib.lk_paged_prefill_workspace(at_zero) == pairs * 2 * 256 * 80 * 4 + pairs * 2 * 8
+    long_chunk = _lib.PrefillShape(2048, 30720, 32, 8, 128, 36, 16, 0, _lib.LK_BF16, _lib.LK_BF16, 128**-0.5)
+    assert lib.lk_paged_prefill_workspace(long_chunk) == 0
+    monkeypatch.setenv("LAYOVER_PREFILL_PAIR_BIAS", "64")  # every cut at or past the heavy tile's end
+    assert lib.lk_paged_prefill_workspace(at_zero) == 0
+    monkeypatch.setenv("LAYOVER_PREFILL_PAIR_BIAS", "12")
+    monkeypatch.setenv("LAYOVER_PREFILL_PAIR_HALVES", "0")
+    assert lib.lk_paged_prefill_workspace(at_zero) == 0
+
+
 def test_fp8_prefill_workspace_holds_the_staged_history(monkeypatch):
     """An FP8-record pool's history is staged as a one-layer BF16 pool (64 KiB a block at
     Qwen3-4B's 8 KV heads) plus an int32 index, each part 256-byte aligned, ahead of any split

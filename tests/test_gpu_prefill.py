@@ -300,3 +300,34 @@ def test_prefill_gives_the_same_bits_on_every_launch(start, tokens, kv_heads, gq
         again = paged_prefill_attention_hip(q, pool, 1, block_ids, start, gqa)
         torch.cuda.synchronize()
         assert torch.equal(again.view(torch.int16), first.view(torch.int16))
+
+
+@pytest.mark.parametrize("bias", [None, "-6", "-40", "30"], ids=["bias_default", "bias_-6", "bias_-40", "bias_30"])
+@pytest.mark.parametrize("fp8", [False, True, "direct"], ids=["bf16_pool", "fp8_pool", "fp8_pool_direct"])
+@pytest.mark.parametrize("start,tokens,kv_heads,gqa", [(0, 512, 4, 4), (300, 421, 2, 3), (0, 200, 8, 4)])
+def test_paired_key_halves_match_the_oracle_and_repeat(start, tokens, kv_heads, gqa, fp8, bias, monkeypatch):
+    """Unsplit chunks whose grid is resident at once divide each heavy tile's key steps between
+    the two workgroups of a CU pair; the side that finishes second merges both states. The
+    split point moves with LAYOVER_PREFILL_PAIR_BIAS (-40: the heavy side keeps one step;
+    30: few or no tiles divide). Results match the oracle, and repeated launches give the same
+    bits although which side merges can change from launch to launch."""
+    from layover_amd.kernels.hip_prefill import paged_prefill_attention_hip
+
+    monkeypatch.setenv("LAYOVER_PREFILL_SPLITS", "1")
+    monkeypatch.setenv("LAYOVER_PREFILL_FP8", "direct" if fp8 == "direct" else "staged")
+    if bias is not None:
+        monkeypatch.setenv("LAYOVER_PREFILL_PAIR_BIAS", bias)
+    end = start + tokens
+    used = -(-end // 16)
+    pool, state = make_pool(used + 1, 2, kv_heads, seed=tokens + kv_heads, fp8=fp8)
+    block_ids = np.random.default_rng(tokens).permutation(used + 1)[:used].astype(np.int32)
+    ids = torch.from_numpy(block_ids).cuda()
+    q = torch.randn(kv_heads * gqa, tokens, 128, generator=torch.Generator().manual_seed(tokens)).to(torch.bfloat16).cuda()
+    print(f"prefill pair halves start={start} tokens={tokens} kv={kv_heads} gqa={gqa} fp8={fp8} bias={bias}", flush=True)
+    first = paged_prefill_attention_hip(q, pool, 1, ids, start, gqa).clone()
+    torch.cuda.synchronize()
+    assert_close(first, oracle.prefill_attention(q.float().cpu().numpy(), state, 1, block_ids, start, gqa))
+    for _ in range(3):
+        again = paged_prefill_attention_hip(q, pool, 1, ids, start, gqa)
+        torch.cuda.synchronize()
+        assert torch.equal(again.view(torch.int16), first.view(torch.int16))
