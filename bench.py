@@ -133,13 +133,18 @@ def measure_link(device, nbytes: int = 512 << 20, repeats: int = 5) -> dict:
     return out
 
 
-def measure_hbm(device, nbytes: int = 8 << 30, repeats: int = 5) -> dict:
+def measure_hbm(device, nbytes: int = 8 << 30, repeats: int = 5, launch_bytes: int = 0, launch_repeats: int = 100) -> dict:
     """HBM ceilings measured on this GPU with the library's streaming probes (non-temporal; a
     read moves 4 KiB per wave, a copy or mix 1 KiB per single-wave workgroup, the faster shape
     for each): read-only over 8 GiB, a copy of 4 GiB
     (8 GiB of traffic), and the two traffic mixes of the FP8 record kernels: 8 GiB read and
     4 GiB written (quantize's 2:1), 4 GiB read and 8 GiB written (dequantize's 1:2). Reported
-    beside the 8 TB/s specification; rates count bytes read plus bytes written."""
+    beside the 8 TB/s specification; rates count bytes read plus bytes written.
+
+    With launch_bytes, the two mixes are also timed at that much traffic per launch (a record
+    kernel's launch), launch_repeats launches back to back over consecutive slices of the 8 GiB
+    buffers, so that each launch pays the dispatch ramp and drain the record kernels pay and
+    reads nothing a cache holds: the like-for-like ceiling for those kernels."""
     import torch
 
     from layover_amd.kernels import _lib
@@ -167,6 +172,27 @@ def measure_hbm(device, nbytes: int = 8 << 30, repeats: int = 5) -> dict:
         end.record()
         end.synchronize()
         out[name] = repeats * moved / (start.elapsed_time(end) * 1e-3) / 1e9
+    if launch_bytes:
+        small = launch_bytes // 3 // 4096 * 4096  # the 1 part of a 2:1 or 1:2 mix, whole pages
+        slots = nbytes // (2 * small)
+        for name, two_to_one in (("quantize_mix_launch_gbs", True), ("dequantize_mix_launch_gbs", False)):
+            src_bytes, dst_bytes = (2 * small, small) if two_to_one else (small, 2 * small)
+
+            def launch(i):
+                k = i % slots
+                _lib.check(lib.lk_stream_probe_mix(src.data_ptr() + k * src_bytes, src_bytes, dst.data_ptr() + k * dst_bytes, dst_bytes, stream))
+
+            for i in range(3):
+                launch(i)
+            torch.cuda.synchronize()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            for i in range(launch_repeats):
+                launch(3 + i)
+            end.record()
+            end.synchronize()
+            out[name] = launch_repeats * 3 * small / (start.elapsed_time(end) * 1e-3) / 1e9
+        out["launch_bytes"] = 3 * small
     del src, dst
     torch.cuda.empty_cache()
     return out
@@ -1110,18 +1136,28 @@ def main() -> None:
 
     # Last, so its 12 GiB of buffers come and go after everything timed above.
     log("HBM probe")
-    result["hbm_probe"] = {k: round(v, 1) for k, v in measure_hbm(device).items()}
+    launch_bytes = int(result["roofline"]["bytes_per_launch"]) if "roofline" in result else 0
+    result["hbm_probe"] = {k: round(v, 1) for k, v in measure_hbm(device, launch_bytes=launch_bytes).items()}
     result["hbm_probe"]["kind"] = (
         "lk_stream_probe: read 8 GiB; copy 4 GiB (8 GiB of traffic); lk_stream_probe_mix: 8 GiB read + 4 GiB written "
-        "(quantize's 2:1), 4 GiB read + 8 GiB written (dequantize's 1:2)"
+        "(quantize's 2:1), 4 GiB read + 8 GiB written (dequantize's 1:2); *_mix_launch_gbs: the same mixes at one "
+        "record launch's traffic per launch (launch_bytes), 100 launches over fresh slices"
     )
     if "roofline" in result:
-        # The quantize kernel against the measured ceiling for its own read/write mix.
+        # The quantize kernel against the measured ceiling for its own read/write mix, streamed
+        # and at its own launch size.
         result["hbm_probe"]["quantize_frac_of_mix"] = round(result["roofline"]["achieved"] / result["hbm_probe"]["quantize_mix_gbs"], 3)
+        result["hbm_probe"]["quantize_frac_of_launch_mix"] = round(
+            result["roofline"]["achieved"] / result["hbm_probe"]["quantize_mix_launch_gbs"], 3
+        )
     if "dequantize_kernel" in result:
         result["hbm_probe"]["dequantize_frac_of_mix"] = round(
             result["dequantize_kernel"]["achieved_gbs"] / result["hbm_probe"]["dequantize_mix_gbs"], 3
         )
+        if "dequantize_mix_launch_gbs" in result["hbm_probe"]:
+            result["hbm_probe"]["dequantize_frac_of_launch_mix"] = round(
+                result["dequantize_kernel"]["achieved_gbs"] / result["hbm_probe"]["dequantize_mix_launch_gbs"], 3
+            )
 
     if not args.skip_cpu:
         log(f"cpu baseline: oracle FP8 quantize+dequantize of all {args.blocks} blocks")
