@@ -74,6 +74,9 @@ struct PrefillArgs {
 // Polls of a partner's ready word (each after a short sleep) before the merging side gives up
 // and writes NaN: about a second, far beyond the microseconds a resident partner needs.
 constexpr uint32_t kPairWaitBound = 1u << 22;
+// A pair's words after its merge: odd with every bit set, never tag | side for an even tag
+// below 2^64 - 2.
+constexpr uint64_t kPairCleared = ~0ull;
 
 // Floats of one workgroup's state in the pair merge: per thread, 64 accumulators of its rows
 // and dims, then the 8 rows' maxima and 8 weight totals, in 16-byte pieces, thread-fastest.
@@ -921,6 +924,13 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
         __syncthreads();
         const bool lost = pair_lost != 0;
         asm volatile("" ::: "memory");
+        // Both words are done with (the partner swapped and published before this side got
+        // here); clearing them lets a launch that repeats this tag, such as a replay of a
+        // captured graph, start clean.
+        if (threadIdx.x == 0) {
+            __hip_atomic_store(a.pair_tags + pair_index, kPairCleared, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(a.pair_ready + pair_index, kPairCleared, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
 #pragma unroll
         for (int set = 0; set < 2; ++set) {
             const f32x4 m_in = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(other, at(16 + set), 0, kAgent));

@@ -331,3 +331,43 @@ def test_paired_key_halves_match_the_oracle_and_repeat(start, tokens, kv_heads, 
         again = paged_prefill_attention_hip(q, pool, 1, ids, start, gqa)
         torch.cuda.synchronize()
         assert torch.equal(again.view(torch.int16), first.view(torch.int16))
+
+
+@pytest.mark.parametrize("fp8", [False, True], ids=["bf16_pool", "fp8_pool"])
+def test_paired_key_halves_replay_in_a_graph(fp8, monkeypatch):
+    """A chunk whose heavy tiles divide, captured in a HIP graph: every replay runs with the
+    launch tag fixed at capture, so the pair words must be left clean by each launch's merges
+    for the next replay to pair up afresh. Before each of four replays the queries change in
+    place and an eager launch (its own workspace) gives the expected output; each replay must
+    equal it bit for bit, which a merge with the previous replay's state would not."""
+    from layover_amd.kernels.hip_prefill import paged_prefill_attention_hip
+
+    monkeypatch.setenv("LAYOVER_PREFILL_SPLITS", "1")
+    monkeypatch.setenv("LAYOVER_PREFILL_PAIR_BIAS", "-6")
+    start, tokens, kv_heads, gqa = 0, 512, 4, 4
+    used = -(-(start + tokens) // 16)
+    pool, state = make_pool(used + 1, 2, kv_heads, seed=77, fp8=fp8)
+    block_ids = np.random.default_rng(77).permutation(used + 1)[:used].astype(np.int32)
+    ids = torch.from_numpy(block_ids).cuda()
+    q = torch.randn(kv_heads * gqa, tokens, 128, generator=torch.Generator().manual_seed(77)).to(torch.bfloat16).cuda()
+    print(f"prefill pair halves in a graph fp8={fp8}", flush=True)
+    eager = paged_prefill_attention_hip(q, pool, 1, ids, start, gqa).clone()
+    torch.cuda.synchronize()
+    assert_close(eager, oracle.prefill_attention(q.float().cpu().numpy(), state, 1, block_ids, start, gqa))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        paged_prefill_attention_hip(q, pool, 1, ids, start, gqa)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = paged_prefill_attention_hip(q, pool, 1, ids, start, gqa)
+    for replay in range(4):
+        # New queries each time, so a merge with a state left by the previous replay would show.
+        q.copy_(torch.randn(q.shape, generator=torch.Generator().manual_seed(100 + replay)).to(torch.bfloat16))
+        expected = paged_prefill_attention_hip(q, pool, 1, ids, start, gqa).clone()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured.view(torch.int16), expected.view(torch.int16))
