@@ -16,6 +16,9 @@ launches are the ones bench.py times:
   and every restored block its dequantize.
 - config 2: the 512-block FP8 swap of the 12 GiB pool through two 128 MiB slots, every record
   and every restored block against the oracle.
+- the paged prefill's three bench chunks (2,048 tokens at 0, where heavy tiles divide within
+  CU pairs; 2,048 ending a 32,768 context; 512 at 8,192 with split keys), BF16 and FP8
+  pools, against the oracle on sampled tokens.
 - a seeded randomized sweep of shapes, lengths, gains and dtypes, after the reference's
   property test (tests/test_triton_decode.py:335-353), and the reference's Qwen3-4B-shape
   case at layers 0, 17 and 35 (tests/test_triton_decode.py:649-684).
@@ -562,3 +565,42 @@ def test_randomized_shapes_match_the_oracle(hip_decode, case):
         assert error.max() < 1e-4 * max(1.0, np.abs(expected).max()), (case, error.max())
     else:
         assert_close(out, expected, str(case))
+
+
+PREFILL_SAMPLES = {
+    # (start, tokens): sampled tokens. At position 0 tiles of 32 tokens (128 rows) pair up on
+    # a CU, and tiles 44-63 (tokens 1,408-2,047) divide their key steps with their partners.
+    (0, 2048): [0, 1, 15, 16, 31, 32, 33, 500, 1023, 1024, 1407, 1408, 1439, 1600, 1800, 2000, 2015, 2016, 2046, 2047],
+    (30720, 2048): [0, 1, 127, 128, 1000, 2047],
+    (8192, 512): [0, 1, 255, 256, 511],
+}
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp8"])
+@pytest.mark.parametrize("start,tokens", list(PREFILL_SAMPLES), ids=lambda v: str(v))
+def test_prefill_at_the_bench_geometry_matches_the_oracle_on_sampled_tokens(hip_decode, pools, kind, start, tokens):
+    """bench.py's three prefill chunks (2,048 tokens at 0 and ending a 32,768 context, 512 at
+    8,192 with its keys split) over the 36-layer Qwen3-4B pool with 0.1% outliers, BF16 and
+    FP8 records (staged as BF16, against the oracle on the dequantized pool): sampled tokens,
+    each one decode row of the float64 oracle (query t sees start + t + 1 keys)."""
+    from layover_amd.kernels.hip_prefill import paged_prefill_attention_hip
+
+    layer = 17
+    end = start + tokens
+    used = -(-end // SLOTS)
+    rng = np.random.default_rng(start + tokens)
+    block_ids = rng.choice(POOL_BLOCKS, used, replace=False).astype(np.int32)
+    gen = torch.Generator(device="cuda").manual_seed(tokens)
+    q = torch.randn(QUERY_HEADS, tokens, DIM, generator=gen, device="cuda").to(torch.bfloat16)
+    log(f"bench-geometry prefill {kind} start={start} tokens={tokens}")
+    pool = pools["bf16"] if kind == "bf16" else pools["fp8"]
+    out = paged_prefill_attention_hip(q, pool, layer, torch.from_numpy(block_ids).cuda(), start, GROUPS)
+    torch.cuda.synchronize()
+    sample = PREFILL_SAMPLES[(start, tokens)]
+    q_bits = q[:, sample].permute(1, 0, 2).contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    reference_pool = layer_bits(pools["bf16" if kind == "bf16" else "dequantized"], layer)
+    table = np.repeat(block_ids[None], len(sample), axis=0)
+    lengths = np.array([start + t + 1 for t in sample], dtype=np.int32)
+    expected = oracle_decode(q_bits, reference_pool, table, lengths)
+    rounding = weight_rounding(q_bits, reference_pool, table, lengths)
+    assert_close(out[:, sample].permute(1, 0, 2), expected, f"prefill {kind} {start}+{tokens}", rounding=np.abs(rounding))
