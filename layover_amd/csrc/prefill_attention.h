@@ -71,8 +71,9 @@ struct PrefillArgs {
     uint64_t* pair_ready;
 };
 
-// Polls of a partner's ready word (each after a short sleep) before the merging side gives up
-// and writes NaN: about a second, far beyond the microseconds a resident partner needs.
+// Polls of a partner's ready word (each a memory round trip after a short sleep) before the
+// merging side gives up and writes NaN: a few seconds, far beyond the microseconds a resident
+// partner needs.
 constexpr uint32_t kPairWaitBound = 1u << 22;
 // A pair's words after its merge: odd with every bit set, never tag | side for an even tag
 // below 2^64 - 2.
@@ -872,8 +873,8 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
         // the XCD's own L2, which other XCDs do not see), waits for every store, and then
         // publishes its tag in the pair's ready word. The second finds the first's tag in the
         // pair's word; the first is then resident and has nothing left to wait for, so the
-        // second waits for the ready word (with a bound that turns a lost partner into NaN
-        // output, not a hang), reads the state with agent-scope loads and merges. The merge
+        // second waits for the ready word (with a bound of a few seconds that turns a lost
+        // partner into NaN output, not a hang), reads the state with agent-scope loads and merges. The merge
         // takes side 1's state first whichever side runs it, so the output bits do not depend
         // on which side arrived last.
         const uint32_t self = job_part[job] - 1;
