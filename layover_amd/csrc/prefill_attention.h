@@ -457,8 +457,37 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
         }
     }
 
+    // Per set: row n's token, head and causal limit; Q as the QK B operand. A job's Q is
+    // loaded before its loop (the first job) or, in the BF16 kernel, as the previous job's loop
+    // ends, so that the round trip overlaps that job's epilogue.
+    int32_t limit[2];
+    uint32_t qt[2][16];
+    auto load_q = [&](uint32_t tile) __attribute__((always_inline)) {
+#pragma unroll
+        for (int set = 0; set < 2; ++set) {
+            const uint32_t row = tile * kLdsWaves * kLdsRows + wave * kLdsRows + 16 * set + n;
+            const bool live = row < total_rows;
+            const uint32_t token = live ? row / a.groups : 0;
+            const uint32_t head = kv_head * a.groups + (live ? row % a.groups : 0);
+            limit[set] = live ? int32_t(a.start + token) : -1;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) qt[set][i] = 0;
+            if (live) {
+                const u32x4* src = reinterpret_cast<const u32x4*>(a.q + (uint64_t(head) * a.tokens + token) * kDim + 32 * g);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const u32x4 w = src[j];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) qt[set][4 * j + i] = w[i];
+                }
+            }
+        }
+    };
+    if constexpr (KV == LK_BF16) load_q(job_tile[0]);
+
     for (uint32_t job = 0; job < jobs; ++job) {
     const uint32_t tile = job_tile[job];
+    if constexpr (KV != LK_BF16) load_q(tile);
     const uint32_t wg_row0 = tile * kLdsWaves * kLdsRows;
     const uint32_t row0 = wg_row0 + wave * kLdsRows;
     // This job's steps [first_step, steps); a split past the tile's keys does none.
@@ -466,29 +495,6 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
     const uint32_t steps = job_last[job];
     // The wave's first row's limit (later rows only see more keys); -1 for a wave past the end.
     const int64_t first_limit = row0 < total_rows ? int64_t(a.start) + row0 / a.groups : -1;
-
-    // Per set: row n's token, head and causal limit; Q as the QK B operand.
-    int32_t limit[2];
-    uint32_t qt[2][16];
-#pragma unroll
-    for (int set = 0; set < 2; ++set) {
-        const uint32_t row = row0 + 16 * set + n;
-        const bool live = row < total_rows;
-        const uint32_t token = live ? row / a.groups : 0;
-        const uint32_t head = kv_head * a.groups + (live ? row % a.groups : 0);
-        limit[set] = live ? int32_t(a.start + token) : -1;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) qt[set][i] = 0;
-        if (live) {
-            const u32x4* src = reinterpret_cast<const u32x4*>(a.q + (uint64_t(head) * a.tokens + token) * kDim + 32 * g);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const u32x4 w = src[j];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) qt[set][4 * j + i] = w[i];
-            }
-        }
-    }
 
     // Cooperative step loads: wave w brings tile w (K0, K1, V0, V1). Chunk x of lane t is
     // values 512x + 8t .. +8 of the tile (16 bytes of BF16, or 8 FP8 codes that become 16
@@ -816,6 +822,11 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
         uint32_t step = first_step;
         for (; step < unmasked; ++step) run_step(step, std::false_type{});
         for (; step < steps; ++step) run_step(step, std::true_type{});
+    }
+    // This job's Q and limits are done with. (The FP8 kernel loads the next job's Q at its
+    // start instead: held across this epilogue it would spill.)
+    if constexpr (KV == LK_BF16) {
+        if (job + 1 < jobs) load_q(job_tile[job + 1]);
     }
 
     if (a.key_splits > 1) {
