@@ -899,7 +899,11 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
         // Thread t's 16-byte piece c sits at (256 c + t) x 16: pieces 0-15 the accumulators
         // o[set][e] (rows 4g + r), 16-17 the rows' maxima, 18-19 their weight totals.
         constexpr int kAgent = 16;  // cache policy: coherent at agent scope (past the XCD's L2)
-        const auto at = [&](uint32_t piece) __attribute__((always_inline)) { return (piece * kWave * kLdsWaves + threadIdx.x) * 16; };
+        // The thread's byte offset in a vector register (an opaque copy, so that it is formed
+        // here and not held through the step loop), the piece's in the scalar offset operand.
+        uint32_t thread_at = threadIdx.x * 16;
+        asm volatile("" : "+v"(thread_at));
+        const auto piece_at = [](uint32_t piece) { return int(piece * kWave * kLdsWaves * 16); };
         f32x4 row_m[2], totals[2];
 #pragma unroll
         for (int set = 0; set < 2; ++set)
@@ -917,9 +921,9 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
 #pragma unroll
             for (int set = 0; set < 2; ++set) {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[set][e]), own, at(set * 8 + e), 0, kAgent);
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, row_m[set]), own, at(16 + set), 0, kAgent);
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, totals[set]), own, at(18 + set), 0, kAgent);
+                for (int e = 0; e < 8; ++e) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o[set][e]), own, thread_at, piece_at(set * 8 + e), kAgent);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, row_m[set]), own, thread_at, piece_at(16 + set), kAgent);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, totals[set]), own, thread_at, piece_at(18 + set), kAgent);
             }
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
@@ -945,11 +949,11 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
         }
 #pragma unroll
         for (int set = 0; set < 2; ++set) {
-            const f32x4 m_in = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(other, at(16 + set), 0, kAgent));
-            const f32x4 total_in = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(other, at(18 + set), 0, kAgent));
+            const f32x4 m_in = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(other, thread_at, piece_at(16 + set), kAgent));
+            const f32x4 total_in = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(other, thread_at, piece_at(18 + set), kAgent));
             f32x4 o_in[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) o_in[e] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(other, at(set * 8 + e), 0, kAgent));
+            for (int e = 0; e < 8; ++e) o_in[e] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(other, thread_at, piece_at(set * 8 + e), kAgent));
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const float m0 = self == 0 ? row_m[set][r] : m_in[r], m1 = self == 0 ? m_in[r] : row_m[set][r];
