@@ -763,8 +763,8 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
         // first. Measured on MI355X (2,048 tokens ending a 32,768 context): 1.094 -> 1.023 ms
         // per layer; raising it for the QK MFMAs instead, or dropping it around set 0's PV, was
         // 1.08-1.11 and 1.07 ms. With the steps paired it still gains 1-2% there (1.059-1.067
-        // against 1.079-1.081 ms on one box), and under the max-ilp scheduling this file builds
-        // with (0.991-1.001 against 1.003-1.010 ms).
+        // against 1.079-1.081 ms on one box), and under the max-ilp scheduling the prefill kernels
+        // build with (0.991-1.001 against 1.003-1.010 ms).
         __builtin_amdgcn_s_setprio(1);
         top[0] = lane_max(s[0], f);
         if constexpr (kMasked) {
