@@ -45,9 +45,9 @@ struct PrefillPlan {
 
 // Steps moved toward the heavy side of a divided tile (the partner side pays a second
 // prologue and epilogue); LAYOVER_PREFILL_PAIR_BIAS overrides it, read per launch. Measured on
-// MI355X, 2,048 tokens at position 0: 0.053-0.055 ms per layer at 6-16, 0.051 at 18, 0.051-0.053
-// at 20-26 (two or three runs each on one box).
-constexpr int32_t kPairBias = 18;
+// MI355X, 2,048 tokens at position 0 (partner on the heavy remainder first): 0.049-0.051 ms per
+// layer at 8, 0.049 at 10, 0.050-0.051 at 12, 0.050-0.052 at 14-16 (two runs each, one box).
+constexpr int32_t kPairBias = 10;
 
 // Key steps of a 128-row tile of the LDS kernel, and whether a CU pair divides its heavy
 // tile: the same arithmetic as prefill_mfma_lds's job plan.

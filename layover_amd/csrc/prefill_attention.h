@@ -55,8 +55,8 @@ struct PrefillArgs {
     // Paired key halves (paired grids without key splits, given a workspace). A CU pair is a
     // heavy tile's workgroup (order < half) and its partner (order + half), which takes the
     // light tile. When the heavy tile has more steps than half the pair's work, the heavy
-    // workgroup stops at about that half and the partner, after its light tile, takes the heavy
-    // tile's remaining steps. Each side writes its unnormalized state to
+    // workgroup stops at about that half and the partner takes the heavy tile's remaining
+    // steps, then its own light tile. Each side writes its unnormalized state to
     // pair_state[(kv head, pair, side)] and swaps pair_tag | side into
     // pair_tags[(kv head, pair)] (pair: the light tile's index); the side that finds its
     // partner's tag of this launch there merges both, in side order, and writes out. Only the
@@ -447,11 +447,20 @@ __global__ __launch_bounds__(kWave* kLdsWaves) __attribute__((amdgpu_waves_per_e
                     job_last[0] = cut;
                     job_part[0] = 1;
                 } else {
+                    // The heavy tile's remaining steps first, its own light tile after: its
+                    // state is then out early and the heavy side, which finishes later,
+                    // merges. Measured on MI355X (2,048 tokens at position 0): 0.049 ms per
+                    // layer against 0.051-0.052 with the light tile first (each at its best
+                    // pair_bias).
                     jobs = 2;
-                    job_tile[1] = heavy;
-                    job_first[1] = cut;
-                    job_last[1] = heavy_steps;
-                    job_part[1] = 2;
+                    job_tile[1] = job_tile[0];
+                    job_first[1] = job_first[0];
+                    job_last[1] = job_last[0];
+                    job_part[1] = 0;
+                    job_tile[0] = heavy;
+                    job_first[0] = cut;
+                    job_last[0] = heavy_steps;
+                    job_part[0] = 2;
                 }
             }
         }
