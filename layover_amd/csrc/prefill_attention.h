@@ -1027,6 +1027,14 @@ __global__ __launch_bounds__(kWave * 4) void prefill_merge(PrefillArgs a) {
     if (unit >= uint64_t(a.kv_heads) * total_rows) return;
     const uint32_t kv_head = uint32_t(unit / total_rows), row = uint32_t(unit % total_rows);
     const uint64_t base = unit * a.key_splits;
+    // The first kEarly splits' accumulators are loaded before (m, l) is combined, so that both
+    // loads are one round trip.
+    constexpr uint32_t kEarly = 8;
+    float early[kEarly][2];
+#pragma unroll
+    for (uint32_t s = 0; s < kEarly; ++s)
+#pragma unroll
+        for (int i = 0; i < 2; ++i) early[s][i] = s < a.key_splits ? a.partial_acc[(base + s) * kDim + lane + kWave * i] : 0.0f;
     const float lane_m = lane < a.key_splits ? a.partial_ml[2 * (base + lane)] : kNoMax;
     const float lane_l = lane < a.key_splits ? a.partial_ml[2 * (base + lane) + 1] : 0.0f;
     float top = lane_m;
@@ -1038,7 +1046,13 @@ __global__ __launch_bounds__(kWave * 4) void prefill_merge(PrefillArgs a) {
     for (int mask = 32; mask >= 1; mask >>= 1) total += __shfl_xor(total, mask, kWave);
     const float inverse = 1.0f / total;
     float sum[2] = {0.0f, 0.0f};
-    for (uint32_t s = 0; s < a.key_splits; ++s) {
+#pragma unroll
+    for (uint32_t s = 0; s < kEarly; ++s) {
+        const float w = __shfl(weight, int(s), kWave);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) sum[i] = s < a.key_splits ? fmaf(w, early[s][i], sum[i]) : sum[i];
+    }
+    for (uint32_t s = kEarly; s < a.key_splits; ++s) {
         const float w = __shfl(weight, int(s), kWave);
         const float* acc = a.partial_acc + (base + s) * kDim;
 #pragma unroll
