@@ -202,8 +202,8 @@ int lk_paged_decode_append(const lk_decode_shape* shape, const void* q, void* po
 /* No counterpart in the reference. lk_paged_decode for callers that cannot allocate device
  * memory (code under HIP graph capture, serving loops that forbid hipMalloc): the same
  * arguments minus the workspace, whose split partials go to a file-scope device array of
- * 16 MiB per GPU (held until the process ends; its address is looked up on the first call
- * on each device). A shape whose lk_paged_decode_workspace exceeds 16 MiB is refused with
+ * 32 MiB per GPU (held until the process ends; its address is looked up on the first call
+ * on each device). A shape whose lk_paged_decode_workspace exceeds 32 MiB is refused with
  * LK_ERR_INVALID. Calls on one GPU share the array, so they are ordered: a call on a stream
  * other than the previous call's first makes its stream wait for that call (an event recorded
  * after each call; one event per device, created on the first call). Under HIP graph capture

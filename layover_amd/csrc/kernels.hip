@@ -152,7 +152,10 @@ Geometry geometry(const lk_decode_shape& s, const void* pool = nullptr) {
     // At most 256 blocks per split: the fast kernel's waves hold their block ids one per lane.
     //
     // Blocks per split, a power of two in [8, 256]. Large batches aim at about 4,096
-    // workgroups (at least 64 blocks each). A grid that would leave CUs idle instead takes
+    // workgroups (at least 64 blocks each); FP8 records, whose tiles are half the bytes, at
+    // about 8,192: batch 32 at 1,024-32,768 tokens on distinct blocks 189.7 -> 186 us per layer,
+    // on shared blocks 153 -> 151.5 us, with 64 blocks a split instead of 128 (the same change
+    // slowed the BF16 decode, 288 -> 291.6 us on shared blocks). A grid that would leave CUs idle instead takes
     // about one workgroup per CU: measured per layer at batch 1, 4,096 tokens 19.9 -> 12.8 us
     // (BF16) with 16 splits instead of 4, and at 16,384 tokens 22.3 -> 20.3 us. An FP8-record
     // table of at most 64 blocks stays one split, which writes the output itself with no merge
@@ -161,7 +164,8 @@ Geometry geometry(const lk_decode_shape& s, const void* pool = nullptr) {
     uint32_t bps = env_bps() > 256 ? 256 : env_bps();
     if (bps == 0) {
         const uint64_t work = units * s.table_width;
-        const uint64_t large = (work + 4095) / 4096;
+        const uint64_t target = s.kv_format == LK_FP8_RECORD ? 8192 : 4096;
+        const uint64_t large = (work + target - 1) / target;
         const uint64_t fill = (work + compute_units() - 1) / compute_units();
         const uint64_t wanted = s.kv_format == LK_FP8_RECORD && s.table_width <= 64 ? 64 : std::max(large, std::min<uint64_t>(fill, 64));
         bps = 8;
@@ -653,7 +657,7 @@ LK_EXPORT int lk_paged_decode_append(const lk_decode_shape* shape, const void* q
 // caller's rule). The stream must belong to the current device, whose array is used.
 namespace lk {
 
-constexpr uint64_t kStaticScratchBytes = 16ull << 20;
+constexpr uint64_t kStaticScratchBytes = 32ull << 20;
 constexpr int kMaxDevices = 64;
 
 static __device__ __align__(256) uint8_t decode_scratch[kStaticScratchBytes];

@@ -9,7 +9,7 @@ launches are the ones bench.py times:
 - config 4: the same kernel over FP8 records (576 groups per block, 0.1% outliers at +/-40):
   batch 1 at 32,768, batch 64 at 4,096 and batch 32 mixed, against the oracle run on the
   dequantized pool.
-- the fused token write (lk_paged_decode_append) at 128- and 256-block splits and with more
+- the fused token write (lk_paged_decode_append) at 64- to 256-block splits and with more
   than 64 splits at 8 KV heads, BF16 and FP8, against the two-launch sequence and the oracle.
 - config 5: decode steps computed while 2,048 blocks swap out as FP8 records and back in equal
   the same steps computed alone, bit for bit; every swapped record equals the oracle's quantize
@@ -209,20 +209,28 @@ def test_config4_fp8_records_match_the_oracle_on_the_dequantized_pool(hip_decode
     if lengths is None:
         lengths = mixed_lengths(13, 32)
         lengths[3] = 32768
-    splits = {"batch1_32768": 32, "batch64_4096": 4, "batch32_mixed": 16}[case]
+    splits = {"batch1_32768": 32, "batch64_4096": 4, "batch32_mixed": 32}[case]
     run_case(hip_decode, pools, "fp8", lengths, seed=len(case), layers=(0, 35), expect_splits=splits)
 
 
-@pytest.mark.parametrize("fp8", [False, True], ids=["bf16_pool", "fp8_pool"])
-@pytest.mark.parametrize("batch", [32, 64])
+# (FP8 records?, batch): the split count the plan gives, 2,048 // blocks per split. FP8 records
+# aim at twice the workgroups, so their 256-block splits need batch 128.
+LONG_SPLITS = {(False, 32): 16, (False, 64): 8, (True, 32): 32, (True, 64): 16, (True, 128): 8}
+
+
+@pytest.mark.parametrize("fp8,batch", list(LONG_SPLITS), ids=lambda v: str(v))
 def test_fused_write_at_long_splits_equals_two_launches_and_the_oracle(hip_decode, pools, fp8, batch):
-    """lk_paged_decode_append at 128-block (batch 32) and 256-block (batch 64) splits: each row
+    """lk_paged_decode_append at long splits: 128- and 256-block splits on the BF16 pool (batch
+    32, 64), 64-, 128- and 256-block splits on FP8 records (batch 32, 64, 128). Each row
     writes one new token at its last position, into a block no other row holds. Pool bytes
     and outputs equal write-then-decode launched separately, and outputs match the oracle on
     the written pool."""
     rng = np.random.default_rng(20 + batch)
-    lengths = mixed_lengths(20 + batch, batch)
-    lengths[1] = 32768
+    # Rows up to the full 2,048-block width, or as long as the pool allows once every row has
+    # a last block of its own (batch 128 leaves 1,984 blocks); row 1 the longest.
+    cap = min(32768, (POOL_BLOCKS - batch) * SLOTS)
+    lengths = [min(n, cap) for n in mixed_lengths(20 + batch, batch)]
+    lengths[1] = cap
     last = np.arange(POOL_BLOCKS - batch, POOL_BLOCKS)
     table = tables_for(rng, lengths, POOL_BLOCKS, reserved_last=last)
     lens = np.array(lengths, dtype=np.int32)
@@ -240,7 +248,7 @@ def test_fused_write_at_long_splits_equals_two_launches_and_the_oracle(hip_decod
     else:
         fused_pool, split_pool = pools["bf16"].clone(), pools["bf16"].clone()
     splits = splits_of(hip_decode, q, fused_pool, table_gpu, lens_gpu)
-    assert splits == {32: 16, 64: 8}[batch]
+    assert splits == LONG_SPLITS[(fp8, batch)]
     log(f"fused write+decode fp8={fp8} batch {batch} splits {splits}")
     fused, separate = torch.empty_like(q), torch.empty_like(q)
     hip_decode.run_kernel_append(q, fused_pool, layer, table_gpu, lens_gpu, GROUPS, write_blocks, write_slots, k, v, fused)
